@@ -1,0 +1,150 @@
+"""Block-scaled W8A8 linears on the MI355X int8 / fp8 matrix cores (gfx950 HIP kernels).
+
+Drop-in for the reference's `hy_nomas/kernels.py` (same names, arguments and return values):
+
+    y[m, n] = sum_g  a_scale[m, g] * w_scale[n, g] * sum_{k in g} qa[m, k] * qw[n, k]   (+ bias[n])
+
+int8: absmax / 127, round half away from zero, exact int32 products per group.
+fp8:  absmax / 448 (OCP e4m3fn), fp32 accumulation.
+
+The group is 128 channels (the reference's layout: scales [rows, K / 128]).  A scale tensor with a single
+column selects one scale per token (activations) or per output channel (weights); the GEMM then
+accumulates the whole K in int32 and dequantizes once.  Weights are used as stored.
+"""
+import torch
+
+from . import _lib
+
+GROUP = 128
+EPILOGUES = {None: 0, "gelu": 1, "gelu_quant": 2}
+
+
+def _aligned(t, bytes_):
+    return t.data_ptr() % bytes_ == 0
+
+
+def _rows(x):
+    """x with unit column stride, 16-byte aligned rows (copy only if needed)."""
+    if x.stride(-1) != 1 or not _aligned(x, 16) or (x.stride(0) * x.element_size()) % 16:
+        x = x.contiguous()
+    return x
+
+
+def quantize_activations(x, kind="int8", group=GROUP, rounding="half_away"):
+    """x [M, K] (K % 128 == 0) -> codes [M, K] and fp32 scales [M, K / group] (hy_nomas/kernels.py:45-54).
+
+    `group=None` (or K) gives one scale per token; `rounding="half_even"` switches the int8 rounding."""
+    _lib.require_device(x)
+    m, k = x.shape
+    g = k if group is None else group
+    dtype = torch.int8 if kind == "int8" else torch.float8_e4m3fn
+    q = torch.empty((m, k), device=x.device, dtype=dtype)
+    s = torch.empty((m, k // g), device=x.device, dtype=torch.float32)
+    if m == 0:
+        return q, s
+    x = _rows(x)
+    _lib.call("hn_quantize_act", x.data_ptr(), _lib.dtype_code(x), x.stride(0), m, k, g, _lib.KIND[kind],
+              _lib.ROUND[rounding], q.data_ptr(), q.stride(0), s.data_ptr(), s.stride(0), _lib.stream(x))
+    return q, s
+
+
+def _scales(s, rows, groups):
+    """fp32 [rows, groups] with unit column stride; a single column is broadcast to `groups` columns."""
+    s = s.float()
+    if s.shape[1] != groups:
+        if s.shape[1] != 1:
+            raise RuntimeError(f"scale tensor with {s.shape[1]} columns, expected {groups} or 1")
+        s = s.expand(rows, groups)
+    if s.stride(1) != 1:
+        s = s.contiguous()
+    return s
+
+
+def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8", epilogue=None):
+    """Block-scaled GEMM on quantized activations (hy_nomas/kernels.py:152-170).  With epilogue
+    "gelu_quant" returns (int8 [M, N], scales [M, N / 128]) ready for the next int8 linear; otherwise
+    [M, N] in `out_dtype`."""
+    _lib.require_device(qa, sa, qw, sw, bias)
+    m, k = qa.shape
+    n = qw.shape[0]
+    mode = EPILOGUES[epilogue]
+    if mode == 2:
+        out = torch.empty((m, n), device=qa.device, dtype=torch.int8)
+        qs = torch.empty((m, n // GROUP), device=qa.device, dtype=torch.float32)
+    else:
+        out = torch.empty((m, n), device=qa.device, dtype=out_dtype)
+        qs = None
+    if m == 0:
+        return (out, qs) if mode == 2 else out
+    # one scale per token and per channel -> whole-K accumulation; otherwise the g128 fold
+    if sa.shape[1] == 1 and sw.shape[1] == 1:
+        group, groups = k, 1
+    else:
+        group, groups = GROUP, k // GROUP
+    sa = _scales(sa, m, groups)
+    sw = _scales(sw, n, groups)
+    qa = _rows(qa)
+    qw = _rows(qw)
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
+              sw.data_ptr(), sw.stride(0), _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
+              m, n, k, group, _lib.KIND[kind], mode, out.data_ptr(), _lib.dtype_code(out) if mode != 2 else 0,
+              out.stride(0), _lib.ptr(qs), qs.stride(0) if qs is not None else 0, _lib.stream(qa))
+    return (out, qs) if mode == 2 else out
+
+
+def block_gemm_acc32(qa, qw):
+    """Full-K int32 dot products qa @ qw^T of int8 codes (a test hook: the exact integer accumulator)."""
+    _lib.require_device(qa, qw)
+    m, k = qa.shape
+    n = qw.shape[0]
+    out = torch.empty((m, n), device=qa.device, dtype=torch.int32)
+    if m == 0:
+        return out
+    qa = _rows(qa)
+    qw = _rows(qw)
+    _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), None, 0, qw.data_ptr(), qw.stride(0), None, 0, None, 0,
+              m, n, k, k, _lib.KIND["int8"], _lib.EPI_ACC32, out.data_ptr(), 0, out.stride(0), None, 0,
+              _lib.stream(qa))
+    return out
+
+
+def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away"):
+    """x [B, L, D] bf16, shift/scale [B, D] -> int8 codes [B * L, D] and scales [B * L, D / 128] of the
+    modulated LayerNorm (hy_nomas/kernels.py:198-207).  Any D that is a multiple of 128 (e.g. 3072);
+    `norm="rms"` uses RMSNorm instead of LayerNorm."""
+    _lib.require_device(x, shift, scale)
+    b, l, d = x.shape
+    x = x.contiguous()
+    shift = shift.to(x.dtype).contiguous()
+    scale = scale.to(x.dtype).contiguous()
+    q = torch.empty((b * l, d), device=x.device, dtype=torch.int8)
+    s = torch.empty((b * l, d // GROUP), device=x.device, dtype=torch.float32)
+    if b * l == 0:
+        return q, s
+    _lib.call("hn_adaln_quant", x.data_ptr(), shift.data_ptr(), scale.data_ptr(), _lib.dtype_code(x), b, l, d, eps,
+              _lib.NORM[norm], _lib.ROUND[rounding], q.data_ptr(), s.data_ptr(), _lib.stream(x))
+    return q, s
+
+
+def block_linear(x, qw, sw, bias=None, kind="int8"):
+    """F.linear with block-scaled 8-bit weights: x [..., K] -> [..., N] in x's dtype
+    (hy_nomas/kernels.py:210-222).  Weight scales [N, K/128] select per-token-and-group activation
+    quantization; per-channel scales [N, 1] select per-token quantization."""
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    if shape[-1] % GROUP or x2.shape[0] == 0:
+        from .ops import dequantize_g128
+        return torch.nn.functional.linear(x, dequantize_g128(qw, sw, x.dtype), bias)
+    group = None if sw.shape[1] == 1 else GROUP
+    with torch.cuda.device(x.device):
+        qa, sa = quantize_activations(x2, kind, group)
+        out = block_gemm(qa, sa, qw, sw.float(), bias, x.dtype, kind)
+    return out.reshape(*shape[:-1], qw.shape[0])
+
+
+def int8_g128_linear(x, qw, sw, bias=None):
+    return block_linear(x, qw, sw, bias, kind="int8")

@@ -1,0 +1,127 @@
+/*
+ * hynomas.h -- C ABI of the gfx950 (MI355X) kernels for Hy-Nomas' quantized DiT linear path.
+ *
+ * The reference (PedroMarinhoDev/ComfyUI-Hy-Nomas) exposes this path as Python functions backed by
+ * Triton kernels; each entry point below replaces one of them and cites it (reference-tree file:line).
+ * The Python modules hy_nomas/kernels.py, fused.py and ops.py of this package keep the reference's call
+ * signatures and call these entry points through ctypes.
+ *
+ * Conventions shared by every entry point:
+ *   - all tensor arguments are device pointers; sizes and strides are in elements;
+ *   - the last dimension of every matrix is unit-stride; row strides are explicit;
+ *   - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream); the call only enqueues
+ *     work, outputs are owned by the caller, nothing is allocated;
+ *   - the return value is HN_OK or an error code; hn_last_error() describes the last failure of the
+ *     calling thread.  Shapes are validated before any launch.
+ */
+#ifndef HYNOMAS_H
+#define HYNOMAS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum hn_status { HN_OK = 0, HN_ERR_ARG = 1, HN_ERR_HIP = 2, HN_ERR_UNSUPPORTED = 3 };
+
+/* element types of activation / output tensors */
+enum hn_dtype { HN_DTYPE_BF16 = 0, HN_DTYPE_F16 = 1, HN_DTYPE_F32 = 2 };
+
+/* code types of quantized operands: int8, or OCP float8 e4m3fn (torch.float8_e4m3fn) */
+enum hn_kind { HN_KIND_INT8 = 0, HN_KIND_FP8 = 1 };
+
+/* int8 rounding of x / scale: half away from zero (the reference's rule), or half to even */
+enum hn_round { HN_ROUND_HALF_AWAY = 0, HN_ROUND_HALF_EVEN = 1 };
+
+/* GEMM epilogues (kernels.py:149 EPILOGUES) plus a raw int32 accumulator output for testing */
+enum hn_epilogue { HN_EPI_NONE = 0, HN_EPI_GELU = 1, HN_EPI_GELU_QUANT = 2, HN_EPI_ACC32 = 3 };
+
+/* row normalisation of the adaLN kernels: LayerNorm without affine (the reference), or RMSNorm */
+enum hn_norm { HN_NORM_LAYER = 0, HN_NORM_RMS = 1 };
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int hn_version(void);
+
+/* Text of the calling thread's last error ("" if none). */
+const char* hn_last_error(void);
+
+/*
+ * Dynamic activation quantization.  Replaces kernels.quantize_activations / _quantize_kernel
+ * (hy_nomas/kernels.py:22-54).
+ *   x [M, K] (x_dtype, row stride ldx) -> q [M, K] int8 or e4m3 codes (row stride ldq),
+ *   s [M, K / group] fp32 (row stride lds).
+ * group = 128 reproduces the reference (one scale per token and 128 channels); group = K gives one scale
+ * per token.  K % 128 == 0.  int8: scale = absmax / 127 (1 for an all-zero group); fp8: scale =
+ * max(absmax, 1e-12) / 448.
+ */
+int hn_quantize_act(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t group, int kind,
+                    int rounding, void* q, int64_t ldq, float* s, int64_t lds, void* stream);
+
+/*
+ * Block-scaled 8-bit GEMM.  Replaces kernels.block_gemm / _gemm_body (hy_nomas/kernels.py:80-170).
+ *   out[m, n] = sum_g (part_g[m, n] * sa[m, g]) * sw[n, g]  (+ bias[n]),  g over K / group groups,
+ * part_g the exact int32 (int8) or fp32 (fp8) dot product of group g; the sum runs in group order as
+ * acc = fma(part * sa, sw, acc).
+ *   qa [M, K] codes (row stride lda), qw [N, K] codes (row stride ldw, K-major: the NT layout),
+ *   sa [M, K / group] (row stride ldsa), sw [N, K / group] (row stride ldsw), fp32;
+ *   bias [N] of bias_dtype or NULL.
+ * group = 128 (the reference's g128 layout) or K (per-token activations x per-channel weights).
+ * epilogue NONE: out [M, N] of out_dtype.  GELU: out = bf16(gelu_tanh(bf16(acc))) (kernels.py:125-128).
+ * GELU_QUANT: out int8 [M, N] codes of the GELU output, quantized per row and 128 columns, with scales
+ * qs [M, N / 128] (kernels.py:129-137); N % 128 == 0.  ACC32: out int32 [M, N] = full-K integer dot
+ * products (int8 only; a test hook, scales and bias are ignored).
+ * K % 128 == 0; M, N >= 1.
+ */
+int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                  const float* sw, int64_t ldsw, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K,
+                  int64_t group, int kind, int epilogue, void* out, int out_dtype, int64_t ldo, float* qs,
+                  int64_t ldqs, void* stream);
+
+/*
+ * LayerNorm (or RMSNorm) + adaLN modulate.  Replaces fused.adaln / _adaln_kernel (hy_nomas/fused.py:37-62).
+ *   x [B, L, D] contiguous (x_dtype bf16 or fp16), shift/scale [B, D] -> y [B, L, D] (same dtype):
+ *   y = norm(x) * bf16(1 + scale[b]) + shift[b].
+ */
+int hn_adaln(const void* x, const void* shift, const void* scale, int dtype, int64_t B, int64_t L, int64_t D,
+             float eps, int norm, void* y, void* stream);
+
+/*
+ * LayerNorm (or RMSNorm) + modulate + int8 quantization per 128 channels.  Replaces kernels.adaln_quant /
+ * _adaln_quant_kernel (hy_nomas/kernels.py:173-207).  D % 128 == 0 (any multiple, e.g. 3072).
+ *   q [B * L, D] int8, s [B * L, D / 128] fp32 of bf16(norm(x) * bf16(1 + scale) + shift).
+ */
+int hn_adaln_quant(const void* x, const void* shift, const void* scale, int dtype, int64_t B, int64_t L,
+                   int64_t D, float eps, int norm, int rounding, int8_t* q, float* s, void* stream);
+
+/*
+ * Gated residual.  Replaces fused.gated_residual / _gated_residual_kernel (hy_nomas/fused.py:108-128).
+ *   out = x + bf16(y * gate[b]) rounded to the dtype; x, y, out [B, L, D] contiguous, gate [B, D].
+ */
+int hn_gated_residual(const void* x, const void* y, const void* gate, int dtype, int64_t B, int64_t L,
+                      int64_t D, void* out, void* stream);
+
+/*
+ * Per-head RMSNorm + interleaved RoPE.  Replaces fused.qk_norm_rope / _qk_norm_rope_kernel
+ * (hy_nomas/fused.py:65-105).
+ *   x [B, L, H, D] bf16 with token stride ldx (heads contiguous, batch stride L * ldx), weight [D] fp32
+ *   holding the bf16 weight's values, cos/sin [L, D] fp32 or both NULL (no rotation) -> y [B, L, H, D]
+ *   bf16 contiguous.  D in {64, 128, 256}.
+ */
+int hn_qk_norm_rope(const void* x, int64_t ldx, const float* weight, const float* cos_t, const float* sin_t,
+                    int64_t B, int64_t L, int64_t H, int64_t D, float eps, void* y, void* stream);
+
+/*
+ * PixelUMM split-half RMSNorm + sectioned MRoPE.  Replaces fused.pixelumm_qk / _pixelumm_qk_kernel
+ * (hy_nomas/fused.py:131-186).
+ *   x [N, H, D] bf16 with token stride ldx, weight_t / weight_hw [D / 2] fp32 (the weights' values),
+ *   cos/sin [N, D] fp32 -> y [N, H, D] bf16.  D == 128 (PixelUMM's head_dim).
+ */
+int hn_pixelumm_qk(const void* x, int64_t ldx, const void* weight_t, const void* weight_hw, const float* cos_t,
+                   const float* sin_t, int64_t N, int64_t H, int64_t D, float eps, void* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HYNOMAS_H */

@@ -1,0 +1,57 @@
+"""The C-ABI library loads and exports every entry point include/hynomas.h declares (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hynomas.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared()
+    for expected in ("hn_quantize_act", "hn_block_gemm", "hn_adaln", "hn_adaln_quant", "hn_gated_residual",
+                     "hn_qk_norm_rope", "hn_pixelumm_qk", "hn_version", "hn_last_error"):
+        assert expected in names
+
+
+def test_library_exports_every_declared_symbol():
+    import torch  # noqa: F401  (the library binds to torch's HIP runtime)
+    from hy_nomas import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhynomas_hip.so not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) == set(declared())
+
+
+def test_argument_validation_without_a_gpu():
+    """Bad shapes are rejected on the host before any launch, with a message."""
+    import torch  # noqa: F401
+    from hy_nomas import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhynomas_hip.so not built")
+    l = _lib.lib()
+    assert l.hn_version() >= 100
+    rc = l.hn_quantize_act(None, 0, 100, 4, 100, 128, 0, 0, None, 100, None, 1, None)   # K % 128 != 0
+    assert rc == 1 and b"multiple of 128" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, None, 0, 4, 8, 256, 64, 0, 0, None, 0, 8, None, 0,
+                         None)   # group 64
+    assert rc == 1 and b"group" in l.hn_last_error()
+    rc = l.hn_adaln_quant(None, None, None, 0, 1, 4, 200, 1e-6, 0, 0, None, None, None)   # D % 128 != 0
+    assert rc == 1 and b"multiple of 128" in l.hn_last_error()
+    rc = l.hn_qk_norm_rope(None, 96, None, None, None, 1, 1, 1, 96, 1e-6, None, None)   # head dim 96
+    assert rc == 1
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, None, 0, 4, 8, 256, 128, 0, 7, None, 0, 8, None,
+                         0, None)   # bad epilogue
+    assert rc == 1

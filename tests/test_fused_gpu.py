@@ -1,0 +1,144 @@
+"""Fused DiT elementwise kernels on the GPU vs the CPU oracle and the torch arithmetic they replace
+(hy_nomas/fused.py; tolerances of the reference's tests/test_fused.py)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("b,l,d,norm", [(2, 777, 2048, "layer"), (1, 4096, 3072, "layer"), (1, 300, 3072, "rms"),
+                                        (3, 5, 136, "layer")])
+def test_adaln(dev, b, l, d, norm):
+    from hy_nomas import fused
+
+    print(f"adaln b={b} l={l} d={d} norm={norm}", flush=True)
+    g = seeded(b * l + d)
+    # strided input like the reference test: transpose of [B, D, L]
+    x = bf(torch.randn(b, d, l, generator=g) * 3).transpose(1, 2)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    got = fused.adaln(x.to(dev), shift.to(dev), scale.to(dev), norm=norm).cpu()
+    ref = bf(torch.from_numpy(oracle.adaln(x.contiguous(), shift, scale, norm=norm)).view(b, l, d))
+    mismatch = (got != ref).float().mean().item()
+    assert mismatch < 1e-3, mismatch
+    assert (got.float() - ref.float()).abs().max().item() < 0.05
+
+
+def test_adaln_matches_torch(dev):
+    """hy_nomas tests/test_fused.py:12-21 against torch's F.layer_norm + modulate on the CPU."""
+    from hy_nomas import block, fused
+
+    g = seeded(1)
+    x = bf(torch.randn(2, 2048, 777, generator=g) * 3).transpose(1, 2)
+    shift = bf(torch.randn(2, 2048, generator=g))
+    scale = bf(torch.randn(2, 2048, generator=g))
+    ref = bf(block.modulate(block.layer_norm(x), shift, scale))
+    got = fused.adaln(x.to(dev), shift.to(dev), scale.to(dev)).cpu()
+    assert (got != ref).float().mean().item() < 1e-3
+    assert (got.float() - ref.float()).abs().max().item() < 0.05
+
+
+@pytest.mark.parametrize("b,l,d,norm", [(1, 300, 2048, "layer"), (1, 2048, 3072, "layer"), (2, 100, 3072, "rms"),
+                                        (1, 64, 12288, "layer")])
+def test_adaln_quant(dev, b, l, d, norm):
+    from hy_nomas import kernels
+
+    print(f"adaln_quant b={b} l={l} d={d} norm={norm}", flush=True)
+    g = seeded(l + d)
+    x = bf(torch.randn(b, d, l, generator=g) * 3).transpose(1, 2)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), norm=norm)
+    q_ref, s_ref, _ = oracle.adaln(x.contiguous(), shift, scale, norm=norm, quant=True)
+    assert (q.cpu().numpy() != q_ref).mean() < 1e-3
+    assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-3)
+
+
+def test_adaln_quant_matches_unfused(dev):
+    """hy_nomas tests/test_fused.py:52-60."""
+    from hy_nomas import fused, kernels
+
+    g = seeded(2)
+    x = bf(torch.randn(1, 2048, 300, generator=g) * 3).transpose(1, 2).to(dev)
+    shift = bf(torch.randn(1, 2048, generator=g)).to(dev)
+    scale = bf(torch.randn(1, 2048, generator=g)).to(dev)
+    q, s = kernels.adaln_quant(x, shift, scale)
+    q_ref, s_ref = kernels.quantize_activations(fused.adaln(x, shift, scale).view(-1, 2048))
+    assert (q != q_ref).float().mean().item() < 1e-3
+    assert torch.allclose(s, s_ref, rtol=1e-3)
+
+
+@pytest.mark.parametrize("b,l,d", [(1, 500, 2048), (2, 1000, 3072), (1, 3, 8)])
+def test_gated_residual_bit_exact(dev, b, l, d):
+    """hy_nomas tests/test_fused.py:43-49: bit-exact against torch's bf16 arithmetic (and the oracle)."""
+    from hy_nomas import fused
+
+    g = seeded(l)
+    x = bf(torch.randn(b, d, l, generator=g)).transpose(1, 2)   # strided, like the patch embed
+    y = bf(torch.randn(b, l, d, generator=g))
+    gate = bf(torch.randn(b, d, generator=g))
+    got = fused.gated_residual(x.to(dev), y.to(dev), gate.to(dev))
+    ref_gpu = x.to(dev) + y.to(dev) * gate.to(dev).unsqueeze(1)
+    assert torch.equal(got, ref_gpu)
+    assert torch.equal(got.cpu(), bf(torch.from_numpy(oracle.gated_residual(x, y, gate))))
+
+
+def test_qk_norm_rope(dev):
+    """hy_nomas tests/test_fused.py:24-40 tolerances, against torch RMSNorm + apply_rope and the oracle."""
+    from hy_nomas import block, fused
+
+    b, l, h, d = 2, 96, 16, 128
+    g = seeded(3)
+    lin = bf(torch.randn(b, l, h * d, generator=g) * 5)
+    x = lin.view(b, l, h, d)
+    norm = block.RMSNorm(d).bfloat16()
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(d, generator=g) + 0.5)
+    rope = block.rope_freqs([16, 56, 56], 256, 4, 4, 6)
+    with torch.no_grad():
+        ref = block.apply_rope(norm(x).to(torch.bfloat16), *rope)
+        ref_plain = norm(x).to(torch.bfloat16)
+    got = fused.qk_norm_rope(x.to(dev), norm.weight.detach().to(dev), (rope[0].to(dev), rope[1].to(dev))).cpu()
+    got_plain = fused.qk_norm_rope(x.to(dev), norm.weight.detach().to(dev), None).cpu()
+    assert (got_plain != ref_plain).float().mean().item() < 1e-3
+    assert (got != ref).float().mean().item() < 1e-2
+    assert ((got.float() - ref.float()).norm() / ref.float().norm()).item() < 1e-3
+    ora = bf(torch.from_numpy(oracle.qk_norm_rope(x, norm.weight.detach(), rope)))
+    assert (got != ora).float().mean().item() < 1e-2
+
+
+def test_qk_norm_rope_strided_qkv(dev):
+    """q/k as strided views of one QKV GEMM output (token stride 3*H*D), as the block harness calls it."""
+    from hy_nomas import fused
+
+    b, l, h, d = 1, 77, 24, 128
+    g = seeded(4)
+    qkv = bf(torch.randn(b, l, 3, h, d, generator=g) * 2)
+    w = bf(torch.rand(d, generator=g) + 0.5)
+    got = fused.qk_norm_rope(qkv.to(dev)[:, :, 1], w.to(dev), None).cpu()
+    ref = bf(torch.from_numpy(oracle.qk_norm_rope(qkv[:, :, 1].contiguous(), w, None)))
+    assert (got != ref).float().mean().item() < 1e-3
+
+
+def test_pixelumm_qk(dev):
+    from hy_nomas import fused
+
+    n, h, d = 200, 8, 128
+    g = seeded(5)
+    x = bf(torch.randn(1, n, h, d, generator=g) * 3)
+    wt = bf(torch.rand(d // 2, generator=g) + 0.5)
+    whw = bf(torch.rand(d // 2, generator=g) + 0.5)
+    ang = torch.rand(n, d, generator=g) * 6.28
+    cos, sin = ang.cos(), ang.sin()
+    got = fused.pixelumm_qk(x.to(dev), wt.to(dev), whw.to(dev), cos.to(dev), sin.to(dev)).cpu()
+    ref = bf(torch.from_numpy(oracle.pixelumm_qk(x, wt, whw, cos, sin)))
+    assert (got != ref).float().mean().item() < 1e-2
+    assert ((got.float() - ref.float()).norm() / ref.float().norm()).item() < 1e-3

@@ -1,0 +1,180 @@
+"""Block-scaled int8 / fp8 GEMM on the GPU vs the CPU oracle (hy_nomas/kernels.py:80-170).
+
+int8: the int32 accumulators are exact and the fp32 epilogue runs the oracle's operation sequence, so the
+outputs must match the oracle bit for bit.  gelu uses the device expf, so its bf16 outputs may differ
+in rare last-bit cases (the reference test's tolerances apply).  fp8: fp32 accumulation inside the
+matrix core has its own order; checked to 1e-2 max-abs-rel against the fp64 product of the dequantized
+operands (and tightly against the oracle)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import seeded
+from test_quant_gpu import outlier_input
+
+pytestmark = pytest.mark.gpu
+
+
+def int8_weights(n, k, seed, per_channel=False):
+    g = seeded(seed)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    if per_channel:
+        sw = (torch.rand(n, 1, generator=g) * 4e-3 + 1e-3).float()
+    else:
+        sw = (torch.rand(n, k // 128, generator=g) * 4e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    return w, sw, bias
+
+
+def fp64_dequant_product(qa, sa, qw, sw, bias, kind="int8"):
+    """(qa * sa)(qw * sw)^T + b in float64 (the dequantized-operand product)."""
+    if kind == "fp8":
+        table = oracle.e4m3_decode_table().astype(np.float64)
+        a = table[np.asarray(qa).view(np.uint8)]
+        w = table[np.asarray(qw).view(np.uint8)]
+    else:
+        a = np.asarray(qa, dtype=np.float64)
+        w = np.asarray(qw, dtype=np.float64)
+    k = a.shape[1]
+    ra = np.repeat(np.asarray(sa, np.float64), k // sa.shape[1], axis=1)
+    rw = np.repeat(np.asarray(sw, np.float64), k // sw.shape[1], axis=1)
+    out = (a * ra) @ (w * rw).T
+    if bias is not None:
+        out += oracle.to_f32(bias).astype(np.float64)
+    return out
+
+
+def max_abs_rel(got, ref):
+    return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 200, 256), (513, 768, 3072), (64, 256, 12288), (1, 3072, 128)])
+def test_acc32_exact(dev, m, n, k):
+    from hy_nomas import kernels
+
+    print(f"acc32 m={m} n={n} k={k}", flush=True)
+    g = seeded(m + n + k)
+    qa = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+    qw = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    got = kernels.block_gemm_acc32(qa.to(dev), qw.to(dev)).cpu().numpy()
+    ref = qa.numpy().astype(np.int64) @ qw.numpy().astype(np.int64).T
+    assert np.array_equal(got.astype(np.int64), ref)
+
+
+def test_acc32_extreme_codes(dev):
+    """All +-127 codes over K = 12288: the largest accumulator magnitude (198 M) stays exact."""
+    from hy_nomas import kernels
+
+    k = 12288
+    qa = torch.full((32, k), 127, dtype=torch.int8)
+    qa[1::2] = -127
+    qw = torch.full((256, k), -127, dtype=torch.int8)
+    got = kernels.block_gemm_acc32(qa.to(dev), qw.to(dev)).cpu().numpy().astype(np.int64)
+    ref = qa.numpy().astype(np.int64) @ qw.numpy().astype(np.int64).T
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("m,n,k,per_channel", [
+    (300, 384, 1024, False), (257, 3072, 3072, False), (1, 256, 128, False), (1024, 640, 2048, False),
+    (512, 1024, 3072, True), (100, 384, 12288, True), (1024, 3072, 3072, True)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_int8_gemm_bit_exact(dev, m, n, k, per_channel, with_bias):
+    from hy_nomas import kernels
+
+    print(f"int8 gemm m={m} n={n} k={k} per_channel={per_channel} bias={with_bias}", flush=True)
+    x = outlier_input(m, k, seed=m + n)
+    w, sw, bias = int8_weights(n, k, seed=n + k, per_channel=per_channel)
+    bias = bias if with_bias else None
+    group = None if per_channel else 128
+    qa, sa = oracle.quantize(x, group or k)
+    out = kernels.block_gemm(torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev),
+                             bias.to(dev) if bias is not None else None)
+    ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias) if bias is not None else None)
+    ref_bf16 = torch.from_numpy(ref).to(torch.bfloat16)
+    got = out.cpu()
+    diff = (got != ref_bf16).nonzero()
+    assert diff.numel() == 0, f"{len(diff)} outputs differ from the oracle, first {diff[:3].tolist()}"
+    # and the north-star bar against the dequantized-operand product
+    assert max_abs_rel(got.float().numpy(), fp64_dequant_product(qa, sa, w.numpy(), sw.numpy(), bias)) < 1e-2
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_int8_gemm_out_dtypes(dev, out_dtype):
+    from hy_nomas import kernels
+
+    m, n, k = 200, 512, 2048
+    x = outlier_input(m, k, seed=11)
+    w, sw, bias = int8_weights(n, k, seed=12)
+    qa, sa = oracle.quantize(x)
+    out = kernels.block_gemm(torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev),
+                             bias.to(dev), out_dtype=out_dtype)
+    ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    assert torch.equal(out.cpu(), torch.from_numpy(ref).to(out_dtype))
+
+
+def test_int8_gemm_ragged_n(dev):
+    """N not a multiple of 4 or of the tile: the scalar store path."""
+    from hy_nomas import kernels
+
+    m, n, k = 77, 301, 512
+    x = outlier_input(m, k, seed=13)
+    w, sw, bias = int8_weights(n, k, seed=14)
+    qa, sa = oracle.quantize(x)
+    out = kernels.block_gemm(torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev),
+                             bias.to(dev))
+    ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    assert torch.equal(out.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_gelu_epilogues(dev, per_channel):
+    """hy_nomas tests/test_fused.py:63-78 tolerances, against the oracle's epilogue."""
+    from hy_nomas import kernels
+
+    m, k, n = 1000, 2048, 1024
+    x = outlier_input(m, k, seed=21)
+    w, sw, bias = int8_weights(n, k, seed=22, per_channel=per_channel)
+    group = None if per_channel else 128
+    qa, sa = oracle.quantize(x, group or k)
+    args = (torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev), bias.to(dev))
+    gelu = kernels.block_gemm(*args, epilogue="gelu").cpu()
+    ref = torch.from_numpy(oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias), epilogue="gelu"))
+    ref = ref.to(torch.bfloat16)
+    assert (gelu != ref).float().mean().item() < 1e-3
+    assert (gelu.float() - ref.float()).abs().max().item() <= 2 ** -6 * ref.float().abs().max().item()
+    qh, sh = kernels.block_gemm(*args, epilogue="gelu_quant")
+    q_ref, s_ref, _ = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias), epilogue="gelu_quant")
+    assert (qh.cpu().numpy() != q_ref).mean() < 1e-3
+    assert np.allclose(sh.cpu().numpy(), s_ref, rtol=1e-3)
+    # gelu_quant codes are exactly the quantization of this same GEMM's gelu output
+    q2, s2 = kernels.quantize_activations(gelu.to(dev))
+    assert torch.equal(qh.cpu(), q2.cpu()) and torch.equal(sh.cpu(), s2.cpu())
+
+
+@pytest.mark.parametrize("m,n,k,group", [(300, 512, 1024, 128), (1024, 1536, 3072, 128), (200, 384, 2048, None)])
+def test_fp8_gemm(dev, m, n, k, group):
+    from hy_nomas import kernels, pixelumm
+
+    print(f"fp8 gemm m={m} n={n} k={k} group={group}", flush=True)
+    g = seeded(m + n + k)
+    x = outlier_input(m, k, seed=m)
+    wf = torch.randn(n, k, generator=g) * 0.02
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    qw, sblk = pixelumm.quantize_fp8_block(wf)
+    if group is None:
+        sw = sblk.repeat_interleave(128, 0)[:, :1].contiguous()   # one scale per channel
+        # only valid when a block row has one scale: use the first column's scale for the whole row
+        wq_codes = qw
+        sw_full = sw
+    else:
+        sw_full = sblk.repeat_interleave(128, 0)
+        wq_codes = qw
+    qa, sa = oracle.quantize(x, group or k, "fp8")
+    out = kernels.block_gemm(torch.from_numpy(qa).view(torch.float8_e4m3fn).to(dev), torch.from_numpy(sa).to(dev),
+                             wq_codes.to(dev), sw_full.to(dev), bias.to(dev), kind="fp8").cpu().float().numpy()
+    w_codes = wq_codes.view(torch.uint8).numpy()
+    ref = oracle.block_gemm(qa, sa, w_codes, sw_full.numpy(), oracle.to_f32(bias), kind="fp8")
+    exact = fp64_dequant_product(qa, sa, w_codes, sw_full.numpy(), bias, kind="fp8")
+    assert max_abs_rel(out, exact) < 1e-2
+    assert max_abs_rel(out, ref) < 4e-3

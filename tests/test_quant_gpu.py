@@ -1,0 +1,101 @@
+"""Activation quantization on the GPU vs the CPU oracle: bit-exact codes and scales
+(hy_nomas/kernels.py:22-54)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def outlier_input(m, k, seed=0, dtype=torch.bfloat16):
+    """~N(0, 1) with 1% of channels scaled x20 (the benchmark's activation distribution)."""
+    g = seeded(seed)
+    x = torch.randn(m, k, generator=g)
+    ch = torch.randperm(k, generator=g)[: max(1, k // 100)]
+    x[:, ch] *= 20
+    return x.to(dtype)
+
+
+def check_quant(x, dev, kind="int8", group=128, rounding="half_away"):
+    from hy_nomas import kernels
+
+    print(f"quant case kind={kind} group={group} rounding={rounding} shape={tuple(x.shape)} dtype={x.dtype}",
+          flush=True)
+    q, s = kernels.quantize_activations(x.to(dev), kind, group, rounding)
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize(x, group or x.shape[1], kind, rounding)
+    got_q = q.cpu().view(torch.uint8 if kind == "fp8" else torch.int8).numpy()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32)), "scales differ"
+    bad = np.argwhere(got_q != q_ref)
+    assert bad.size == 0, f"{len(bad)} codes differ, first at {bad[:3].tolist()}"
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("m,k", [(1, 128), (7, 256), (300, 2048), (1024, 3072), (33, 12288)])
+def test_quant_g128(dev, kind, m, k):
+    check_quant(outlier_input(m, k, seed=m + k), dev, kind, 128)
+
+
+@pytest.mark.parametrize("kind", ["int8", "fp8"])
+@pytest.mark.parametrize("m,k", [(1, 128), (5, 384), (300, 2048), (1024, 3072), (65, 12288)])
+def test_quant_per_token(dev, kind, m, k):
+    check_quant(outlier_input(m, k, seed=m * k), dev, kind, None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quant_input_dtypes(dev, dtype):
+    check_quant(outlier_input(129, 1024, seed=3, dtype=dtype), dev, "int8", 128)
+    check_quant(outlier_input(129, 1024, seed=4, dtype=dtype), dev, "fp8", None)
+
+
+def test_quant_half_even(dev):
+    check_quant(outlier_input(200, 3072, seed=5), dev, "int8", 128, "half_even")
+    check_quant(outlier_input(200, 3072, seed=6), dev, "int8", None, "half_even")
+
+
+def test_quant_ties_and_zero_groups(dev):
+    # peak 127 -> scale exactly 1: every k + 0.5 is a tie that must round away from zero
+    k = 256
+    x = torch.zeros(4, k)
+    ties = torch.arange(-126.5, 127.0, 1.0)[:128]
+    x[0, :128] = ties
+    x[0, 0] = 127.0
+    x[1, 128:] = -ties.flip(0)
+    x[1, 200] = -127.0
+    x[2] = 0.0                                  # all-zero row: scale 1, codes 0
+    x[3, :128] = torch.tensor([2.0 ** -120] * 128)  # tiny values (the division fallback path)
+    x[3, 128:] = -1e-38
+    x = x.to(torch.bfloat16)
+    for group in (128, None):
+        check_quant(x, dev, "int8", group)
+        check_quant(x, dev, "fp8", group)
+        check_quant(x, dev, "int8", group, "half_even")
+
+
+def test_quant_strided_rows(dev):
+    from hy_nomas import kernels
+
+    big = outlier_input(100, 4096, seed=7)
+    x = big.to(dev)[:, 512:512 + 2048]         # row stride 4096, unit column stride
+    q, s = kernels.quantize_activations(x)
+    q_ref, s_ref = oracle.quantize(big[:, 512:512 + 2048])
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_fp8_encoding_every_bf16(dev):
+    """Every finite bf16 value quantized with scale 1 (group peak 448) must encode like torch's e4m3fn cast."""
+    from hy_nomas import kernels
+
+    bits = torch.arange(0, 0x10000, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = bits.float()
+    vals = vals[torch.isfinite(vals) & (vals.abs() <= 448)]
+    n = (vals.numel() // 127) * 127
+    rows = vals[:n].view(-1, 127)
+    x = torch.cat([rows, torch.full((rows.shape[0], 1), 448.0)], dim=1).to(torch.bfloat16)  # peak 448
+    q, s = kernels.quantize_activations(x.to(dev), "fp8", 128)
+    assert torch.all(s.cpu() == 1.0)
+    ref = x.float().to(torch.float8_e4m3fn).view(torch.uint8)
+    assert torch.equal(q.cpu().view(torch.uint8), ref)
