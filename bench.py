@@ -1,0 +1,270 @@
+"""Benchmark of the quantized DiT linear path on one MI355X.
+
+Headline (one "step"): the DiT-block linear stack at M = 32768 tokens, hidden 3072 -- QKV 3072->9216,
+attention-out 3072->3072, FFN-up 3072->12288, FFN-down 12288->3072 -- as W8A8 int8 GEMMs with per-token
+int8 activations (already quantized and resident in HBM), per-channel int8 weights, bf16 bias and bf16
+outputs.  value = 2*M*N*K summed over the four GEMMs / step time, in TOPS (10^12 int8 ops/s).
+
+The same JSON line carries:
+  roofline      the GEMM kernel's achieved TOPS from per-launch HIP events vs the dense int8 MFMA peak;
+  cpu_baseline  the reference's CPU fallback (dequantize the weight, bf16 F.linear) on a bounded row sample
+                of the same four GEMMs, timed on this host;
+  extra         the stack with activation quantization included, the reference's g128 scale layout,
+                the block-scaled fp8 GEMMs, and the fused elementwise kernels' HBM bandwidth.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "comfyui-hy-nomas_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import torch  # noqa: E402
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+M = 32768
+HIDDEN = 3072
+STACK = [("qkv", 3072, 9216), ("attn_out", 3072, 3072), ("ffn_up", 3072, 12288), ("ffn_down", 12288, 3072)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def outlier_activations(m, k, gen, dev):
+    """bf16 ~N(0, 1) with 1% of the channels scaled x20."""
+    x = torch.randn(m, k, generator=gen, device=dev)
+    ch = torch.randperm(k, generator=gen, device=dev)[: k // 100]
+    x[:, ch] *= 20
+    return x.to(torch.bfloat16)
+
+
+def make_linear(n, k, gen, dev, groups):
+    w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+    sw = torch.rand(n, groups, generator=gen, device=dev) * 4e-3 + 1e-3
+    bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    return w, sw.float(), bias
+
+
+def time_launches(fns, steps, warmup):
+    """Run the list of launches `steps` times; returns (ms per step, [avg ms per launch]) from HIP events
+    recorded on the current stream (the stream the kernels are launched on)."""
+    for _ in range(warmup):
+        for f in fns:
+            f()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in fns]
+          for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for s in range(steps):
+        for i, f in enumerate(fns):
+            ev[s][i][0].record(stream)
+            f()
+            ev[s][i][1].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    per = [sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(steps)) / steps for i in range(len(fns))]
+    return start.elapsed_time(end) / steps, per
+
+
+def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8"):
+    """Headline stack.  Returns (ms/step, per-GEMM ms, total ops, [(name, K, N)])."""
+    from hy_nomas import kernels
+
+    fns, ops, keep = [], 0, []
+    for name, k, n in STACK:
+        x = outlier_activations(M, k, gen, dev)
+        if kind == "int8":
+            groups = 1 if group_mode == "per_token" else k // 128
+            qa, sa = kernels.quantize_activations(x, "int8", None if group_mode == "per_token" else 128)
+            w, sw, bias = make_linear(n, k, gen, dev, groups)
+        else:
+            from hy_nomas import pixelumm
+            qa, sa = kernels.quantize_activations(x, "fp8", 128)
+            wf = torch.randn(n, k, generator=gen, device=dev) * 0.02
+            w, sblk = pixelumm.quantize_fp8_block(wf)
+            sw = sblk.repeat_interleave(128, 0).contiguous()
+            bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+            del wf
+        del x
+        keep.append((qa, sa, w, sw, bias))
+        fns.append(lambda qa=qa, sa=sa, w=w, sw=sw, bias=bias: kernels.block_gemm(qa, sa, w, sw, bias, kind=kind))
+        ops += 2 * M * n * k
+    ms, per = time_launches(fns, steps, warmup)
+    del keep, fns
+    torch.cuda.empty_cache()
+    return ms, per, ops
+
+
+def linear_stack_with_quant(dev, gen, steps, warmup):
+    """The four linears from bf16 activations: per-token quantization + GEMM each (block_linear)."""
+    from hy_nomas import kernels
+
+    fns, keep = [], []
+    for name, k, n in STACK:
+        x = outlier_activations(M, k, gen, dev)
+        w, sw, bias = make_linear(n, k, gen, dev, 1)
+        keep.append((x, w, sw, bias))
+        fns.append(lambda x=x, w=w, sw=sw, bias=bias: kernels.block_linear(x, w, sw, bias))
+    ms, _ = time_launches(fns, steps, warmup)
+    del keep, fns
+    torch.cuda.empty_cache()
+    return ms
+
+
+def elementwise(dev, gen, steps, warmup):
+    """Fused elementwise kernels at x [1, 32768, 3072] bf16, three rotating input sets (576 MiB > the 256 MB
+    Infinity Cache) so each launch reads cold HBM.  Returns {name: (us, GB/s, algorithmic bytes)}."""
+    from hy_nomas import fused, kernels
+
+    n_el = M * HIDDEN
+    sets = []
+    for _ in range(3):
+        x = torch.randn(1, M, HIDDEN, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.randn(1, M, HIDDEN, generator=gen, device=dev).to(torch.bfloat16)
+        sets.append((x, y))
+    shift = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    scale = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    gate = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    cases = {
+        "adaln": (lambda s: fused.adaln(s[0], shift, scale), 4.0),
+        "gated_residual": (lambda s: fused.gated_residual(s[0], s[1], gate), 6.0),
+        "adaln_quant": (lambda s: kernels.adaln_quant(s[0], shift, scale), 3.0 + 4.0 / 128),
+        "quantize_g128": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN)), 3.0 + 4.0 / 128),
+        "quantize_per_token": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN), "int8", None),
+                               3.0 + 4.0 / HIDDEN),
+    }
+    out = {}
+    for name, (fn, bpe) in cases.items():
+        fns = [lambda s=s, fn=fn: fn(s) for s in sets]
+        _, per = time_launches(fns, steps, warmup)
+        us = 1e3 * sum(per) / len(per)
+        nbytes = bpe * n_el
+        out[name] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                     "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3), "bytes": int(nbytes)}
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(target_s=10.0):
+    """The reference's CPU fallback (hy_nomas/ops.py:172-176: dequantize the g128 int8 weight to bf16, then
+    F.linear) on a row sample of the four GEMMs; rows are scaled so the timed work is ~target_s."""
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    layers = []
+    for name, k, n in STACK:
+        w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+        sw = torch.rand(n, k // 128, generator=g) * 4e-3 + 1e-3
+        bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+        layers.append((k, n, w, sw, bias))
+
+    def run(rows):
+        t0 = time.perf_counter()
+        for k, n, w, sw, bias in layers:
+            x = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+            oracle.dequant_linear(x, w, sw, bias)
+        return time.perf_counter() - t0
+
+    rows = 64
+    dt = run(rows)                  # warm-up pass, also sizes the sample
+    rows = int(max(64, min(M, rows * target_s / max(dt, 1e-3) / 3)))
+    reps = 3 if dt * rows / 64 < target_s else 1
+    times = [run(rows) for _ in range(reps)]
+    dt = sorted(times)[len(times) // 2]
+    ops = sum(2 * rows * n * k for _, k, n in STACK)
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{rows} token rows of each of the 4 GEMMs (M=32768 full), median of {reps}, "
+                      f"{dt:.2f} s per pass; dequantize_g128 + bf16 F.linear"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the quantized linear path is single-GPU here (token-parallel "
+              "sharding needs no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    log("bench: int8 per-token x per-channel stack")
+    ms, per, ops = gemm_stack(dev, gen, args.steps, args.warmup)
+    value = ops / (ms * 1e-3) / 1e12
+    kernel_ms = sum(per)
+    achieved = ops / (kernel_ms * 1e-3) / 1e12
+    per_gemm = {name: {"ms": round(t, 4), "TOPS": round(2 * M * n * k / (t * 1e-3) / 1e12, 1)}
+                for (name, k, n), t in zip(STACK, per)}
+    result = {
+        "metric": "W8A8 GEMM TOPS & % int8 MFMA peak; DiT-block linear-stack ms at M=32768",
+        "value": round(value, 1),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "DiT-block W8A8 linear stack, M=32768 tokens, hidden 3072: QKV 3072->9216, "
+                               "attn-out 3072->3072, FFN-up 3072->12288, FFN-down 12288->3072; per-token int8 "
+                               "activations x per-channel int8 weights, bf16 bias, bf16 out",
+                   "M": M, "hidden": HIDDEN, "ops_per_step": ops, "frac_int8_peak": round(value / PEAK_INT8_TOPS, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 3), "traffic": None,
+                     "kernel": "block_gemm_kernel (int8, per-token)", "per_gemm": per_gemm},
+    }
+    if not args.no_extra:
+        extra = {}
+        log("bench: stack with activation quantization")
+        ms_q = linear_stack_with_quant(dev, gen, max(5, args.steps // 2), 2)
+        extra["linear_stack_with_act_quant"] = {"ms": round(ms_q, 4), "TOPS": round(ops / (ms_q * 1e-3) / 1e12, 1)}
+        log("bench: int8 g128 stack")
+        ms_g, per_g, _ = gemm_stack(dev, gen, max(5, args.steps // 2), 2, group_mode="g128")
+        extra["int8_g128_stack"] = {"ms": round(ms_g, 4), "TOPS": round(ops / (ms_g * 1e-3) / 1e12, 1),
+                                    "frac_int8_peak": round(ops / (ms_g * 1e-3) / 1e12 / PEAK_INT8_TOPS, 3),
+                                    "per_gemm_ms": [round(t, 4) for t in per_g]}
+        log("bench: fp8 block-scaled stack")
+        ms_f, per_f, _ = gemm_stack(dev, gen, max(5, args.steps // 2), 2, kind="fp8")
+        fp8 = {}
+        for (name, k, n), t in zip(STACK, per_f):
+            fp8[name] = {"ms": round(t, 4), "TFLOPS": round(2 * M * n * k / (t * 1e-3) / 1e12, 1)}
+        extra["fp8_block_gemm"] = {"per_gemm": fp8, "stack_ms": round(ms_f, 4),
+                                   "frac_fp8_peak": round(ops / (ms_f * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 3)}
+        log("bench: elementwise")
+        extra["elementwise"] = elementwise(dev, gen, max(10, args.steps), 3)
+        result["extra"] = extra
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
