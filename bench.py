@@ -33,6 +33,9 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 M = 32768
 HIDDEN = 3072
+# Memory-side bytes per headline step (4 GEMM launches) from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
+# script, scaled by a plain-copy calibration (FETCH x2.0, WRITE x1.0); profiles/block_gemm_int8_per_token_M32768.md
+TRAFFIC_BYTES_PER_STEP = 7.26e9
 STACK = [("qkv", 3072, 9216), ("attn_out", 3072, 3072), ("ffn_up", 3072, 12288), ("ffn_down", 12288, 3072)]
 
 
@@ -200,6 +203,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of 512 MiB five times (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the quantized linear path is single-GPU here (token-parallel "
@@ -211,6 +216,14 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev).manual_seed(0)
+    if args.calibrate_copy:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(), "launches": 5}))
+        return
 
     log("bench: int8 per-token x per-channel stack")
     ms, per, ops = gemm_stack(dev, gen, args.steps, args.warmup)
@@ -237,7 +250,8 @@ def main():
                                "activations x per-channel int8 weights, bf16 bias, bf16 out",
                    "M": M, "hidden": HIDDEN, "ops_per_step": ops, "frac_int8_peak": round(value / PEAK_INT8_TOPS, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 3), "traffic": None,
+                     "frac": round(achieved / PEAK_INT8_TOPS, 3), "traffic": TRAFFIC_BYTES_PER_STEP,
+                     "traffic_unit": "bytes per step of 4 GEMM launches (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
                      "kernel": "block_gemm_kernel (int8, per-token)", "per_gemm": per_gemm},
     }
     if not args.no_extra:
