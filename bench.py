@@ -36,6 +36,7 @@ HIDDEN = 3072
 # Memory-side bytes per headline step (4 GEMM launches) from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
 # script, scaled by a plain-copy calibration (FETCH x2.0, WRITE x1.0); profiles/block_gemm_int8_per_token_M32768.md
 TRAFFIC_BYTES_PER_STEP = 7.26e9
+SLEEP_CYCLES = 2e8           # ~0.1 s of spin before each timed region
 STACK = [("qkv", 3072, 9216), ("attn_out", 3072, 3072), ("ffn_up", 3072, 12288), ("ffn_down", 12288, 3072)]
 
 
@@ -70,6 +71,9 @@ def time_launches(fns, steps, warmup):
           for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    # a spin kernel holds the GPU while the host queues every timed launch, so the events measure GPU time
+    # and not the host's per-call overhead (which exceeds a 50 us elementwise kernel)
+    torch.cuda._sleep(int(SLEEP_CYCLES))
     start.record(stream)
     for s in range(steps):
         for i, f in enumerate(fns):

@@ -3,7 +3,7 @@
 // Row kernels (adaLN, adaLN+quant): one wavefront per token row; the row is loaded once with 16-byte
 // loads, kept in registers for the mean / variance / output passes, and the statistics are wave
 // reductions.  Head kernels (QK norm + RoPE): D/8 lanes per (token, head), 16 bytes per lane.
-// The gated residual is a flat 16-byte streaming kernel.  All are single-pass and HBM-bound.
+// The gated residual streams rows with 16-byte accesses.  All are single-pass and HBM-bound.
 #include "hn_common.h"
 
 namespace hn {
@@ -20,93 +20,171 @@ __device__ __forceinline__ uint4 narrow8(const float* f) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// value rounding to the tensor dtype, kept in fp32
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (DT == HN_DTYPE_BF16) return rbf16(v);
+  else return f16_bits_to_f32(f32_to_f16_bits(v));
+}
+
+// 8 fp32 values -> 8 packed 2-byte values.  FINITE: the values are known not to be NaN, so the hardware
+// bf16 conversion (equal to the torch rule on every non-NaN value) is used.
+template <int DT, bool FINITE>
+__device__ __forceinline__ uint4 narrow8x(const float* f) {
+  if constexpr (DT == HN_DTYPE_BF16 && FINITE)
+    return make_uint4(bf16x2_finite(f[0], f[1]), bf16x2_finite(f[2], f[3]), bf16x2_finite(f[4], f[5]),
+                      bf16x2_finite(f[6], f[7]));
+  else
+    return narrow8<DT>(f);
+}
+
+// ---------------------------------------------------------------------------------------------
 // adaLN: y = norm(x) * rbf16(1 + scale[b]) + shift[b]          (fused.py:37-52)
 // adaLN + quant: y = rbf16(...), then int8 per 128 channels      (kernels.py:173-195)
-constexpr int kRowThreads = 256;
+//
+// One wavefront per token row, 8 rows per block, all rows of a block in one batch b.  Each wave issues its
+// row's loads first; meanwhile the block stages b's modulation factors g = rbf16(1 + scale[b]) and
+// h = shift[b] as fp32 in LDS, in four planes of D/8 float4 (g[0:4], g[4:8], h[0:4], h[4:8] of each
+// 8-channel chunk) so a wave's reads are consecutive 16-byte slots.  Rows whose statistics are not
+// finite (NaN / inf inputs) take the exact software rounding.
+constexpr int kRowWaves = 8;
+constexpr int kRowThreads = kRowWaves * 64;
 
-template <int DT, int NORM, bool QUANT, int ROUND, int CPL>
+template <int DT, int NORM, bool QUANT, int ROUND, int CPL, bool FULL>
 __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ shift,
-                                                            const uint16_t* __restrict__ scale, int64_t rows,
-                                                            int64_t L, int64_t D, float eps,
+                                                            const uint16_t* __restrict__ scale, int64_t L,
+                                                            int64_t D, float eps, int blocks_per_batch,
                                                             uint16_t* __restrict__ y, int8_t* __restrict__ q,
                                                             float* __restrict__ s) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
-  if (r >= rows) return;  // whole wave exits together
-  const int64_t b = r / L;
-  const int64_t nchunk = D / 8;
-  const uint16_t* xr = x + r * D;
+  extern __shared__ float4 fac[];
+  const int nchunk = (int)(D / 8);
+  const int64_t b = blockIdx.x / blocks_per_batch;
+  const int jb = blockIdx.x % blocks_per_batch;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t l = (int64_t)jb * kRowWaves + wave;
+  const bool live = l < L;  // whole wave
+  const int64_t r = b * L + (live ? l : L - 1);
+  auto has = [&](int i) { return FULL || lane + 64 * i < nchunk; };
   uint4 xv[CPL];
 #pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    int64_t c = lane + 64 * i;
-    if (c < nchunk) xv[i] = *reinterpret_cast<const uint4*>(xr + c * 8);
+  for (int i = 0; i < CPL; i++)
+    if (has(i)) xv[i] = *reinterpret_cast<const uint4*>(x + r * D + (lane + 64 * i) * 8);
+
+  int fin = 1;
+  for (int c = threadIdx.x; c < nchunk; c += kRowThreads) {
+    float sc[8], sh[8], g[8];
+    widen8<DT>(*reinterpret_cast<const uint4*>(scale + b * D + c * 8), sc);
+    widen8<DT>(*reinterpret_cast<const uint4*>(shift + b * D + c * 8), sh);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      g[j] = rbf16(1.0f + sc[j]);
+      fin &= __builtin_isfinite(g[j]) && __builtin_isfinite(sh[j]);
+    }
+    fac[c] = make_float4(g[0], g[1], g[2], g[3]);
+    fac[nchunk + c] = make_float4(g[4], g[5], g[6], g[7]);
+    fac[2 * nchunk + c] = make_float4(sh[0], sh[1], sh[2], sh[3]);
+    fac[3 * nchunk + c] = make_float4(sh[4], sh[5], sh[6], sh[7]);
   }
-  // statistics in fp32: per-lane sums, then a wave reduction
+  const bool fac_finite = __syncthreads_and(fin);
+  if (!live) return;
+
+  // Rows of up to 4096 channels are widened once into fp32 registers; wider rows stay packed and are
+  // widened in each pass.
+  constexpr bool KEEP = CPL <= 8;
+  float f[KEEP ? CPL : 1][8];
+  if constexpr (KEEP) {
+#pragma unroll
+    for (int i = 0; i < CPL; i++)
+      if (has(i)) widen8<DT>(xv[i], f[i]);
+  }
+  // value j of chunk i of the row
+  auto val = [&](int i, int j) -> float {
+    if constexpr (KEEP) {
+      return f[i][j];
+    } else {
+      const uint32_t w = (&xv[i].x)[j >> 1];
+      if constexpr (DT == HN_DTYPE_BF16) return __uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16));
+      else return f16_bits_to_f32((j & 1) ? (w >> 16) : (w & 0xffffu));
+    }
+  };
+  // statistics in fp32: per-lane sums, then a wave reduction (two passes, as the reference); the fp32
+  // copies are centred in place by the second pass
   float mean = 0.0f;
   if constexpr (NORM == HN_NORM_LAYER) {
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < CPL; i++) {
-      if (lane + 64 * i < nchunk) {
-        float f[8];
-        widen8<DT>(xv[i], f);
+    for (int i = 0; i < CPL; i++)
+      if (has(i))
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc += f[j];
-      }
-    }
-    mean = wave_sum(acc) / (float)D;
+        for (int j = 0; j < 8; j++) acc += val(i, j);
+    mean = wave_sum_dpp(acc) / (float)D;
   }
   float sq = 0.0f;
 #pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    if (lane + 64 * i < nchunk) {
-      float f[8];
-      widen8<DT>(xv[i], f);
+  for (int i = 0; i < CPL; i++)
+    if (has(i))
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        float c = f[j] - mean;
+        const float c = val(i, j) - mean;
+        if constexpr (KEEP) f[i][j] = c;
         sq = __builtin_fmaf(c, c, sq);
       }
-    }
-  }
-  const float var = wave_sum(sq) / (float)D;
+  const float var = wave_sum_dpp(sq) / (float)D;
   const float rstd = 1.0f / __builtin_sqrtf(var + eps);
-  const uint16_t* shb = shift + b * D;
-  const uint16_t* scb = scale + b * D;
+  const bool finite = fac_finite && __builtin_isfinite(mean) && __builtin_isfinite(rstd);
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
-    const int64_t c = lane + 64 * i;
-    if (c < nchunk) {
-      float f[8], sh[8], sc[8], o[8];
-      widen8<DT>(xv[i], f);
-      widen8<DT>(*reinterpret_cast<const uint4*>(shb + c * 8), sh);
-      widen8<DT>(*reinterpret_cast<const uint4*>(scb + c * 8), sc);
+    const int c = lane + 64 * i;
+    if (has(i)) {
+      const float4 g0 = fac[c], g1 = fac[nchunk + c], h0 = fac[2 * nchunk + c], h1 = fac[3 * nchunk + c];
+      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+      float o[8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        float n = (f[j] - mean) * rstd;
-        o[j] = n * rbf16(1.0f + sc[j]) + sh[j];
+        const float n = (KEEP ? val(i, j) : val(i, j) - mean) * rstd;
+        o[j] = __builtin_fmaf(n, g[j], h[j]);  // n * rbf16(1 + scale) + shift, contracted as Triton does
       }
       if constexpr (!QUANT) {
-        *reinterpret_cast<uint4*>(y + r * D + c * 8) = narrow8<DT>(o);
+        const uint4 packed = finite ? narrow8x<DT, true>(o) : narrow8x<DT, false>(o);
+        *reinterpret_cast<uint4*>(y + r * D + c * 8) = packed;
       } else {
         float peak = 0.0f;
+        if (__builtin_expect(finite, 1) && DT == HN_DTYPE_BF16) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          o[j] = rbf16(o[j]);
-          peak = __builtin_fmaxf(peak, __builtin_fabsf(o[j]));
+          for (int j = 0; j < 8; j += 2) {
+            const uint32_t w = bf16x2_finite(o[j], o[j + 1]);
+            o[j] = __uint_as_float(w << 16);
+            o[j + 1] = __uint_as_float(w & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; j++) o[j] = rbf16(o[j]);
         }
-        // D % 128 == 0: the 16 lanes of a DPP row hold exactly one 128-channel group
-        peak = row16_max(peak);
-        const float gs = int8_scale(peak);
-        FastDiv div(gs);
-        int cd[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(div(o[j]));
+        for (int j = 0; j < 8; j++) peak = __builtin_fmaxf(peak, __builtin_fabsf(o[j]));  // NaN-free, >= 0
+        // D % 128 == 0: the 16 lanes of a DPP row hold exactly one 128-channel group
+        peak = row16_max_nonneg(peak);
+        float gs;
+        int cd[8];
+        if (__builtin_expect(fast_group(peak), 1)) {
+          gs = int8_scale_fast(peak);
+          const FastDiv<false> div(gs);
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float v = div(o[j]);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+          }
+        } else {
+          gs = int8_scale(peak);
+#pragma unroll
+          for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(o[j] / gs);
+        }
         *reinterpret_cast<uint2*>(q + r * D + c * 8) =
             make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7]));
-        if ((lane & 15) == 0) s[r * (D / 128) + c / 16] = gs;
+        // all 16 lanes of the group store the same scale to the same address (no divergent branch)
+        s[r * (D / 128) + c / 16] = gs;
       }
     }
   }
@@ -115,14 +193,24 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 template <int DT, int NORM, bool QUANT, int ROUND>
 static int launch_adaln(const void* x, const void* shift, const void* scale, int64_t B, int64_t L, int64_t D,
                         float eps, void* y, int8_t* q, float* s, hipStream_t st) {
-  const int64_t rows = B * L;
   const int64_t cpl = (D / 8 + 63) / 64;
-  const unsigned blocks = (unsigned)((rows + 3) / 4);
+  const int64_t per_batch = (L + kRowWaves - 1) / kRowWaves;
+  if (B * per_batch > 0x7fffffff) {
+    set_error("adaln: too many rows (B=%lld, L=%lld)", (long long)B, (long long)L);
+    return HN_ERR_UNSUPPORTED;
+  }
+  const unsigned blocks = (unsigned)(B * per_batch);
+  const size_t lds = (size_t)D * 8;  // four planes of D/8 float4
 #define HN_CASE(N)                                                                                              \
   if (cpl <= N) {                                                                                               \
-    hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N>), dim3(blocks), dim3(kRowThreads), 0, st,       \
-                       (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, rows, L, D, eps,     \
-                       (uint16_t*)y, q, s);                                                                     \
+    if (D == 512 * N)                                                                                           \
+      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, true>), dim3(blocks), dim3(kRowThreads), lds, \
+                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
+                         (int)per_batch, (uint16_t*)y, q, s);                                                   \
+    else                                                                                                        \
+      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, false>), dim3(blocks), dim3(kRowThreads), lds,\
+                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
+                         (int)per_batch, (uint16_t*)y, q, s);                                                   \
     return HN_LAUNCH_CHECK("adaln_kernel");                                                                     \
   }
   HN_CASE(1) HN_CASE(2) HN_CASE(3) HN_CASE(4) HN_CASE(5) HN_CASE(6) HN_CASE(8) HN_CASE(12) HN_CASE(16)
@@ -140,40 +228,58 @@ static int adaln_norm(int norm, const void* x, const void* shift, const void* sc
 }
 
 // ---------------------------------------------------------------------------------------------
-// gated residual: out = x + rbf16(y * gate[b])                   (fused.py:108-118)
-constexpr int kFlatThreads = 256;
-constexpr int kFlatUnroll = 4;
+// gated residual: out = x + round(y * gate[b])                   (fused.py:108-118)
+// A copy-shaped stream: block (64, 4) covers 64 chunks of 8 channels x 4 rows, one 16-byte chunk of x, y
+// and out per thread and row (the gate chunk is an L2 hit); blockIdx.y strides over row groups.  No
+// integer division per element; the batch of a row is computed once per wave.
+constexpr int kGrRows = 4;
 
 template <int DT>
-__global__ __launch_bounds__(kFlatThreads) void gated_residual_kernel(const uint16_t* __restrict__ x,
-                                                                      const uint16_t* __restrict__ yv,
-                                                                      const uint16_t* __restrict__ gate,
-                                                                      uint16_t* __restrict__ out, int64_t nchunk,
-                                                                      int64_t chunks_per_row, int64_t L) {
-  const int64_t base = (int64_t)blockIdx.x * (kFlatThreads * kFlatUnroll) + threadIdx.x;
-  uint4 xv[kFlatUnroll], yvv[kFlatUnroll], gv[kFlatUnroll];
-#pragma unroll
-  for (int u = 0; u < kFlatUnroll; u++) {
-    int64_t c = base + u * kFlatThreads;
-    int64_t cc = c < nchunk ? c : 0;
-    int64_t row = cc / chunks_per_row;
-    int64_t col = cc - row * chunks_per_row;
-    int64_t b = row / L;
-    xv[u] = *reinterpret_cast<const uint4*>(x + cc * 8);
-    yvv[u] = *reinterpret_cast<const uint4*>(yv + cc * 8);
-    gv[u] = *reinterpret_cast<const uint4*>(gate + (b * chunks_per_row + col) * 8);
-  }
-#pragma unroll
-  for (int u = 0; u < kFlatUnroll; u++) {
-    int64_t c = base + u * kFlatThreads;
+__global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ yv,
+                                                             const uint16_t* __restrict__ gate,
+                                                             uint16_t* __restrict__ out, int64_t rows, int64_t L,
+                                                             int cpr) {
+  const int c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= cpr) return;
+  const int64_t D = (int64_t)cpr * 8;
+  for (int64_t r = (int64_t)blockIdx.y * kGrRows + threadIdx.y; r < rows; r += (int64_t)gridDim.y * kGrRows) {
+    const int64_t b = L == rows ? 0 : r / L;  // one batch: no division
+    const uint4 xv = *reinterpret_cast<const uint4*>(x + r * D + c * 8);
+    const uint4 yy = *reinterpret_cast<const uint4*>(yv + r * D + c * 8);
+    const uint4 gv = *reinterpret_cast<const uint4*>(gate + b * D + c * 8);
     float a[8], bb[8], g[8], o[8];
-    widen8<DT>(xv[u], a);
-    widen8<DT>(yvv[u], bb);
-    widen8<DT>(gv[u], g);
+    widen8<DT>(xv, a);
+    widen8<DT>(yy, bb);
+    widen8<DT>(gv, g);
+    bool nan = false;
 #pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = a[j] + rbf16(bb[j] * g[j]);
-    if (c < nchunk) *reinterpret_cast<uint4*>(out + c * 8) = narrow8<DT>(o);
+    for (int j = 0; j < 8; j++) {
+      o[j] = a[j] + round_to<DT>(bb[j] * g[j]);
+      nan |= o[j] != o[j];
+    }
+    uint4 packed;
+    if (__builtin_expect(nan, 0)) packed = narrow8x<DT, false>(o);
+    else packed = narrow8x<DT, true>(o);
+    *reinterpret_cast<uint4*>(out + r * D + c * 8) = packed;
   }
+}
+
+template <int DT>
+static int launch_gated_residual(const void* x, const void* y, const void* gate, int64_t rows, int64_t L, int64_t D,
+                                 void* out, hipStream_t st) {
+  const int64_t cpr = D / 8;
+  if (cpr > 0x7fffffff) {
+    set_error("hn_gated_residual: D too large");
+    return HN_ERR_UNSUPPORTED;
+  }
+  const int64_t gx = (cpr + 63) / 64;
+  int64_t gy = (rows + kGrRows - 1) / kGrRows;
+  gy = gy > 65535 ? 65535 : gy;
+  hipLaunchKernelGGL((gated_residual_kernel<DT>), dim3((unsigned)gx, (unsigned)gy), dim3(64, kGrRows), 0, st,
+                     (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)gate, (uint16_t*)out, rows, L,
+                     (int)cpr);
+  return HN_LAUNCH_CHECK("gated_residual_kernel");
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -325,21 +431,10 @@ extern "C" int hn_gated_residual(const void* x, const void* y, const void* gate,
   HN_REQUIRE(D % 8 == 0, "hn_gated_residual: D=%lld must be a multiple of 8", (long long)D);
   HN_REQUIRE(x && y && gate && out, "hn_gated_residual: null pointer");
   HN_REQUIRE(aligned16(x) && aligned16(y) && aligned16(gate) && aligned16(out), "hn_gated_residual: pointers must be 16-byte aligned");
-  const int64_t nchunk = B * L * D / 8;
-  if (nchunk == 0) return HN_OK;
-  const int64_t per_block = kFlatThreads * kFlatUnroll;
-  const unsigned blocks = (unsigned)((nchunk + per_block - 1) / per_block);
+  if (B * L == 0) return HN_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == HN_DTYPE_BF16) {
-    hipLaunchKernelGGL(gated_residual_kernel<HN_DTYPE_BF16>, dim3(blocks), dim3(kFlatThreads), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)gate, (uint16_t*)out, nchunk, D / 8, L);
-    return HN_LAUNCH_CHECK("gated_residual_kernel");
-  }
-  if (dtype == HN_DTYPE_F16) {
-    hipLaunchKernelGGL(gated_residual_kernel<HN_DTYPE_F16>, dim3(blocks), dim3(kFlatThreads), 0, st,
-                       (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)gate, (uint16_t*)out, nchunk, D / 8, L);
-    return HN_LAUNCH_CHECK("gated_residual_kernel");
-  }
+  if (dtype == HN_DTYPE_BF16) return launch_gated_residual<HN_DTYPE_BF16>(x, y, gate, B * L, L, D, out, st);
+  if (dtype == HN_DTYPE_F16) return launch_gated_residual<HN_DTYPE_F16>(x, y, gate, B * L, L, D, out, st);
   set_error("hn_gated_residual: unsupported dtype %d", dtype);
   return HN_ERR_UNSUPPORTED;
 }

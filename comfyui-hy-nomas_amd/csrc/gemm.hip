@@ -7,26 +7,41 @@ namespace hn {
 // ---------------------------------------------------------------------------------------------
 // configurations
 
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT>
+// Compute units of the current device (the persistent grid has at most one workgroup per CU).
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS>
 static int launch_cfg(GemmArgs& a, hipStream_t st) {
   constexpr int BN = WN * TN * 32, BM = WM * TM * 32;
-  a.tiles_m = (int)((a.M + BM - 1) / BM);
-  a.tiles_n = (int)((a.N + BN - 1) / BN);
-  const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n;
-  if (blocks > 0x7fffffff) {
-    set_error("hn_block_gemm: problem too large (%lld tiles)", (long long)blocks);
+  const int64_t tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+  if (tm * tn > 0x7fffffff) {
+    set_error("hn_block_gemm: problem too large (%lld tiles)", (long long)(tm * tn));
     return HN_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT>), dim3((unsigned)blocks),
+  a.tiles_m = (int)tm;
+  a.tiles_n = (int)tn;
+  const int64_t grid = tm * tn < cu_count() ? tm * tn : cu_count();
+  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS>), dim3((unsigned)grid),
                      dim3(WN * WM * 64), 0, st, a);
   return HN_LAUNCH_CHECK("block_gemm_kernel");
 }
 
 // per-token / per-channel: 256 x 256 tile, 8 waves of 128 x 64.  g128: 256 x 128, 8 waves of 128 x 32.
+// 128-byte K stages in two LDS buffers.
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
-  if (g128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT>(a, st);
-  return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT>(a, st);
+  if (g128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
+  return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
 }
 
 template <int KIND, int EPI>
@@ -73,6 +88,8 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
              "hn_block_gemm: bad bias dtype %d", bias_dtype);
   HN_REQUIRE(lda >= K && ldw >= K && ldo >= N, "hn_block_gemm: row strides smaller than the rows");
   HN_REQUIRE(lda % 16 == 0 && ldw % 16 == 0, "hn_block_gemm: code row strides must be multiples of 16 bytes");
+  HN_REQUIRE(lda < (1 << 22) && ldw < (1 << 22) && ldsa < (1 << 22) && ldsw < (1 << 22) && ldo < (1 << 22),
+             "hn_block_gemm: row strides must be below 2^22 elements");
   HN_REQUIRE(qa && qw && out, "hn_block_gemm: null pointer");
   HN_REQUIRE(((uintptr_t)qa & 15) == 0 && ((uintptr_t)qw & 15) == 0, "hn_block_gemm: codes must be 16-byte aligned");
   if (epilogue != HN_EPI_ACC32) {

@@ -4,18 +4,25 @@
 //
 // Operand roles.  The weight tile is the MFMA "A" operand (rows = output channels n) and the activation
 // tile the "B" operand (columns = tokens m), so each lane of a 32x32 accumulator holds one token and runs
-// of four consecutive output channels: 8-byte bf16 stores along the contiguous N axis of out [M, N].
+// of four consecutive output channels: 8-byte stores along the contiguous N axis of out [M, N].
 //
 // Tiling.  A workgroup owns a BN x BM output tile (BN = WN*TN*32 channels, BM = WM*TM*32 tokens) and walks
-// K in stages of 128 bytes (one g128 group).  Each stage stages the weight and activation tiles in LDS
-// (double buffered; rows of 128 bytes, 16-byte chunks XOR-swizzled by row so that the ds_read_b128 of 8
-// consecutive rows hit 8 distinct bank groups).  Global loads of stage k+1 are issued before the MFMAs
-// of stage k and land in LDS after them, so one barrier per stage suffices.
+// K in stages of BK bytes.  Each stage's weight and activation rows are copied straight from global memory
+// into LDS (gfx950 global_load_lds_dwordx4: no staging registers, no ds_write) into a ring of NS stage
+// buffers, NS - 1 stages ahead of the stage being multiplied, so NS - 1 stages of loads are in flight
+// while the matrix cores work.  One barrier per stage: it publishes stage kt to every wave and retires
+// the buffer of stage kt - 1, which the loads of stage kt + NS - 1 then overwrite.
+//
+// LDS layout.  A stage row of BK bytes is BK / 16 chunks of 16 bytes, XOR-swizzled by row so that the 16
+// lanes the LDS serves together (rows r .. r + 15 of one MFMA fragment read) hit 16 distinct bank
+// groups: chunk c of row r sits at chunk c ^ ((r >> 2) & 3) for 64-byte rows and c ^ ((r >> 1) & 7) for
+// 128-byte rows.  The direct loads write 1 KB per wave instruction in lane order, so the swizzle is
+// applied on the global side: lane i fetches the logical chunk that belongs at its physical slot.
 //
 // Group modes.  group == K (per-token activations x per-channel weights): one integer (int8) or fp32 (fp8)
 // accumulator across the whole K, dequantized once in the epilogue.  group == 128 (the reference's g128
-// layout): each stage produces the group partial, which is folded into an fp32 accumulator with
-// acc = fma(float(part) * sa[m, g], sw[n, g], acc); the per-stage scales ride along in LDS.
+// layout): the stages of one 128-byte group produce its partial, which is folded into an fp32 accumulator
+// with acc = fma(float(part) * sa[m, g], sw[n, g], acc); the group's scales ride along in LDS.
 //
 // Workgroup order.  Consecutive workgroup ids are dealt round-robin to the 8 XCDs; the id is remapped so
 // each XCD owns a contiguous range of tiles, which are then visited in column groups of 8 token tiles so
@@ -47,7 +54,7 @@ struct GemmArgs {
   int stage_store;  // 2-byte out with 16-byte aligned rows and N % 8 == 0: LDS-staged 16-byte stores
 };
 
-constexpr int kBK = 128;      // bytes of K per stage (= one g128 group)
+constexpr int kGroupK = 128;  // bytes of K per scale group (the g128 layout)
 constexpr int kGroupM = 8;    // token tiles per column group in the tile order
 constexpr int kXcds = 8;
 
@@ -57,8 +64,13 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
   return xcd * per + (xcd < rem ? xcd : rem) + local;
 }
 
-// Swizzled byte offset of 16-byte chunk c of tile row `row` (rows are 128 bytes).
-__device__ __forceinline__ int swz(int row, int c) { return row * kBK + ((c ^ (row & 7)) << 4); }
+// Physical chunk of logical 16-byte chunk c in stage row `row` (rows of BK bytes).
+template <int BK>
+__device__ __forceinline__ int swz_chunk(int row, int c) {
+  static_assert(BK == 64 || BK == 128, "stage rows are 64 or 128 bytes");
+  if constexpr (BK == 64) return c ^ ((row >> 2) & 3);
+  else return c ^ ((row >> 1) & 7);
+}
 
 __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) {
   if (dt == HN_DTYPE_BF16) return bf16_bits_to_f32(((const uint16_t*)bias)[n]);
@@ -76,17 +88,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 template <int KIND>
 struct Mfma;
 
-// int8: v_mfma_i32_32x32x32_i8 -- 16 bytes of A and B per lane, 16 int32 accumulators.
+// int8: v_mfma_i32_32x32x32_i8 -- 16 bytes of A and B per lane (logical chunk 2s + lane/32 of slice s),
+// 16 int32 accumulators.
 template <>
 struct Mfma<HN_KIND_INT8> {
   using Frag = v4i;
   using Acc = v16i;
   static constexpr int kSliceK = 32;  // K bytes per instruction
+  template <int BK>
+  __device__ __forceinline__ static Frag load(const char* tile, int row, int slice, int lane) {
+    return *reinterpret_cast<const Frag*>(tile + row * BK + (swz_chunk<BK>(row, slice * 2 + (lane >> 5)) << 4));
+  }
   __device__ __forceinline__ static Acc run(const Frag& a, const Frag& b, const Acc& c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static Frag load(const char* tile, int row, int slice, int lane) {
-    return *reinterpret_cast<const Frag*>(tile + swz(row, slice * 2 + (lane >> 5)));
   }
   __device__ __forceinline__ static float to_f32(int v) { return (float)v; }
   __device__ __forceinline__ static float get(const Acc& c, int r) { return __int_as_float(c[r]); }
@@ -94,23 +108,24 @@ struct Mfma<HN_KIND_INT8> {
 };
 
 // fp8 e4m3: v_mfma_f32_32x32x64_f8f6f4 (format 0 = e4m3 for both operands, no block scales) --
-// 32 bytes of A and B per lane, 16 fp32 accumulators.
+// 32 bytes of A and B per lane (logical chunks 4s + 2 (lane/32) and the next), 16 fp32 accumulators.
 template <>
 struct Mfma<HN_KIND_FP8> {
   using Frag = v8i;
   using Acc = v16f;
   static constexpr int kSliceK = 64;
-  __device__ __forceinline__ static Acc run(const Frag& a, const Frag& b, const Acc& c) {
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-  }
+  template <int BK>
   __device__ __forceinline__ static Frag load(const char* tile, int row, int slice, int lane) {
     const int c0 = slice * 4 + (lane >> 5) * 2;
-    v4i lo = *reinterpret_cast<const v4i*>(tile + swz(row, c0));
-    v4i hi = *reinterpret_cast<const v4i*>(tile + swz(row, c0 + 1));
+    const v4i lo = *reinterpret_cast<const v4i*>(tile + row * BK + (swz_chunk<BK>(row, c0) << 4));
+    const v4i hi = *reinterpret_cast<const v4i*>(tile + row * BK + (swz_chunk<BK>(row, c0 + 1) << 4));
     Frag f;
     f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
     f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
     return f;
+  }
+  __device__ __forceinline__ static Acc run(const Frag& a, const Frag& b, const Acc& c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
   }
   __device__ __forceinline__ static float to_f32(float v) { return v; }
   __device__ __forceinline__ static float get(const Acc& c, int r) { return c[r]; }
@@ -127,301 +142,419 @@ __device__ __forceinline__ void g2lds4(const void* g, char* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_wave_base, 4, 0, 0);
 }
 
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N of this wave's vector-memory loads are outstanding (they retire in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]; others left at max
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT>
-__global__ __launch_bounds__(WN* WM * 64) void block_gemm_kernel(const GemmArgs a) {
+// Workgroup barrier without a memory fence: LDS data published by the barrier is either this kernel's
+// direct loads, retired by wait_vmcnt first, or ds_writes retired by an lgkmcnt wait first.  The memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// 2-byte outputs are converted to bf16 / fp16 two at a time (round to nearest even).
+template <int DT>
+__device__ __forceinline__ uint32_t cvt2_out(float a, float b) {
+  if constexpr (DT == HN_DTYPE_BF16) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+  } else {
+    return pack2_out<DT>(a, b);
+  }
+}
+
+// Persistent kernel: gridDim.x workgroups (at most one per CU) walk the tile list.  Workgroup b runs on
+// XCD b % 8 (the dispatcher deals workgroups to XCDs round-robin); each XCD owns a contiguous range of the
+// tile order, and its workgroups take every nw-th tile of that range, so the tiles in flight on one XCD
+// at any time are consecutive (8 token tiles x 4 channel tiles share their panels in that XCD's L2).
+// The first stage of the next tile is issued before the current tile's epilogue, so its load latency
+// hides behind the epilogue and the epilogue's stores drain while it lands.
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS>
+__global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WN * WM / 4, WN * WM / 4)))
+void block_gemm_kernel(const GemmArgs a) {
   using MF = Mfma<KIND>;
   using Acc = typename MF::Acc;
   using Frag = typename MF::Frag;
   constexpr int NW = WN * WM;
   constexpr int BN = WN * TN * 32, BM = WM * TM * 32;
-  constexpr int A_BYTES = BN * kBK, B_BYTES = BM * kBK;
-  constexpr int SC_BYTES = G128 ? (BN + BM) * 4 : 0;
-  constexpr int STAGE = A_BYTES + B_BYTES + SC_BYTES;
-  constexpr int A_KB = BN / 8 / NW, B_KB = BM / 8 / NW;  // 1 KB direct loads per wave per stage
-  constexpr int SLICES = kBK / MF::kSliceK;
-  static_assert(A_KB * NW * 8 == BN && B_KB * NW * 8 == BM, "tile rows not divisible among waves");
-  static_assert(!G128 || (BN + BM) / 64 <= NW, "not enough waves to stage the scales");
+  constexpr int A_BYTES = BN * BK, B_BYTES = BM * BK;
+  constexpr int SC_SLOTS = (BN + BM) / 64;                   // g128: 64-float scale slots per stage
+  constexpr int SC_PER_WAVE = G128 ? (SC_SLOTS + NW - 1) / NW : 0;
+  constexpr int SC_BYTES = SC_PER_WAVE * NW * 256;           // g128 scales of one stage
+  constexpr int SCR = (NS + 1) * SC_BYTES;                   // the scales' ring, at offset 0
+  constexpr int STAGE = A_BYTES + B_BYTES;                   // operand bytes of one stage buffer
+  constexpr int ROWS_PER_KB = 1024 / BK, CHUNKS = BK / 16;
+  constexpr int A_KB = A_BYTES / 1024 / NW, B_KB = B_BYTES / 1024 / NW;  // 1 KB direct loads per wave
+  constexpr int LOADS = A_KB + B_KB + SC_PER_WAVE;                        // per wave per stage
+  constexpr int SLICES = BK / MF::kSliceK;
+  constexpr int STAGES_PER_GROUP = kGroupK / BK;
+  static_assert(A_KB * NW * 1024 == A_BYTES && B_KB * NW * 1024 == B_BYTES, "tile rows not divisible among waves");
+  static_assert(NS == 2, "two stage buffers: the next tile's first stage fills buffer 0 during the epilogue");
+  static_assert(SLICES >= 2 && SLICES % 2 == 0, "fragment sets alternate per slice, starting each stage at set 0");
+  static_assert(kGroupK % BK == 0, "stage size");
   static_assert(EPI != HN_EPI_GELU_QUANT || TN * 32 == 128, "gelu_quant needs a 128-channel wave tile");
-  // Epilogue staging of 2-byte outputs: each wave transposes its BMW x BNW sub-tile through LDS (token-major
-  // rows padded by 16 bytes) so the stores are full 16-byte lanes along N; the per-channel scales and bias
-  // sit after the staging area.
+  // Epilogue staging of 2-byte outputs, one block of 32 tokens at a time: each wave transposes its
+  // 32 x BNW sub-tile through LDS (token-major rows padded by 16 bytes) so the stores are full 16-byte
+  // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage);
+  // the per-channel scales and bias of the tile follow it.
   constexpr bool STAGED = OUT_DT != HN_DTYPE_F32 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU);
   constexpr int OPITCH = TN * 32 * 2 + 16;
-  constexpr int EP_OFF = STAGED ? NW * TM * 32 * OPITCH : 0;
-  constexpr int SMEM = EP_OFF + 2 * BN * 4 > 2 * STAGE ? EP_OFF + 2 * BN * 4 : 2 * STAGE;
+  constexpr int STG_OFF = SCR + STAGE;
+  constexpr int EP_OFF = STG_OFF + (STAGED ? NW * 32 * OPITCH : 0);
+  constexpr int RING_END = SCR + NS * STAGE;
+  constexpr int SMEM = EP_OFF + 2 * BN * 4 > RING_END ? EP_OFF + 2 * BN * 4 : RING_END;
   __shared__ __align__(16) char smem[SMEM];
 
-  // ---- tile coordinates
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int group_size = kGroupM * a.tiles_n;
-  const int first_m = (logical / group_size) * kGroupM;
-  const int size_m = min(a.tiles_m - first_m, kGroupM);
-  const int tm_idx = first_m + (logical % group_size) % size_m;
-  const int tn_idx = (logical % group_size) / size_m;
-  const int64_t m0 = (int64_t)tm_idx * BM, n0 = (int64_t)tn_idx * BN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave % WN, wm = wave / WN;
 
-  // ---- direct-to-LDS load plan.  Wave w fills the 1 KB blocks q = w + NW * u of each tile; block q is
-  // rows 8q .. 8q+7, and lane i lands in row 8q + i/8 at physical chunk i%8, which holds logical chunk
-  // (i%8) ^ (i/8) under the row swizzle.
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
-  const uint8_t* gw[A_KB];
-  const uint8_t* ga[B_KB];
-#pragma unroll
-  for (int u = 0; u < A_KB; u++) {
-    const int64_t n = min(n0 + (int64_t)(wave + NW * u) * 8 + lrow, a.N - 1);
-    gw[u] = a.qw + n * a.ldw + lchunk * 16;
-  }
-#pragma unroll
-  for (int u = 0; u < B_KB; u++) {
-    const int64_t m = min(m0 + (int64_t)(wave + NW * u) * 8 + lrow, a.M - 1);
-    ga[u] = a.qa + m * a.lda + lchunk * 16;
-  }
-  // g128: waves 0 .. BN/64-1 stage sw[n0 + 64 w + lane, g], the next BM/64 waves sa[m0 + ..., g]
-  const float* gsc = nullptr;
-  int sc_off = 0;
-  if constexpr (G128) {
-    if (wave < BN / 64) {
-      gsc = a.sw + min(n0 + wave * 64 + lane, a.N - 1) * a.ldsw;
-      sc_off = wave * 256;
-    } else if (wave < (BN + BM) / 64) {
-      gsc = a.sa + min(m0 + (wave - BN / 64) * 64 + lane, a.M - 1) * a.ldsa;
-      sc_off = wave * 256;
-    }
-  }
+  // ---- this workgroup's tiles
+  const int G = gridDim.x, b = blockIdx.x;
+  const int xcd = b % kXcds, slot = b / kXcds;
+  const int nwx = G / kXcds + (xcd < G % kXcds ? 1 : 0);
+  const int before = xcd * (G / kXcds) + min(xcd, G % kXcds);
+  const int tiles = a.tiles_m * a.tiles_n;
+  const int t_end = (int)((int64_t)tiles * (before + nwx) / G);
+  int t = (int)((int64_t)tiles * before / G) + slot;
+  if (t >= t_end) return;  // whole workgroup
 
-  auto issue_stage = [&](int kt, int buf) {
-    char* base = smem + buf * STAGE;
-    const int64_t k0 = (int64_t)kt * kBK;
-#pragma unroll
-    for (int u = 0; u < A_KB; u++) g2lds16(gw[u] + k0, base + (wave + NW * u) * 1024);
-#pragma unroll
-    for (int u = 0; u < B_KB; u++) g2lds16(ga[u] + k0, base + A_BYTES + (wave + NW * u) * 1024);
-    if constexpr (G128) {
-      if (gsc) g2lds4(gsc + kt, base + A_BYTES + B_BYTES + sc_off);
-    }
+  auto tile_origin = [&](int tt, int64_t& m0, int64_t& n0) {
+    const int group_size = kGroupM * a.tiles_n;
+    const int first_m = (tt / group_size) * kGroupM;
+    const int size_m = min(a.tiles_m - first_m, kGroupM);
+    m0 = (int64_t)(first_m + (tt % group_size) % size_m) * BM;
+    n0 = (int64_t)((tt % group_size) / size_m) * BN;
   };
 
-  // ---- accumulators
-  Acc acc[TN][TM];                            // MFMA accumulators (whole K, or one group in g128 mode)
-  v16f facc[G128 ? TN : 1][G128 ? TM : 1];    // g128: fp32 running sum over groups
+  // ---- direct-to-LDS load plan.  Wave w fills the 1 KB blocks q = w + NW * u of each tile; block q is
+  // rows q * ROWS_PER_KB + lane / CHUNKS, and lane i lands at physical chunk i % CHUNKS, so it fetches the
+  // logical chunk swz_chunk(row, i % CHUNKS) (the swizzle is an involution).  Rows past M or N re-read
+  // the last row; their products are never stored.
+  // g128: scale slot q < BN/64 holds sw[n0 + 64 q + lane, g], the next BM/64 slots sa[m0 + ..., g]; wave w
+  // fills slots w + NW * u.  Slots past SC_SLOTS load a scale nobody reads, so every wave issues LOADS
+  // loads per stage.
+  // Addresses are a wave-uniform tile base plus a 32-bit per-lane offset (the SGPR-base form of the load).
+  const uint8_t* wbase;
+  const uint8_t* abase;
+  uint32_t woff[A_KB], aoff[B_KB];
+  const float* scbase[SC_PER_WAVE > 0 ? SC_PER_WAVE : 1];
+  uint32_t scoff[SC_PER_WAVE > 0 ? SC_PER_WAVE : 1];
+  auto plan_loads = [&](int64_t m0, int64_t n0, int lane) {
+    wbase = a.qw + n0 * a.ldw;
+    abase = a.qa + m0 * a.lda;
+    const int nlim = (int)min<int64_t>(a.N - 1 - n0, BN - 1), mlim = (int)min<int64_t>(a.M - 1 - m0, BM - 1);
 #pragma unroll
-  for (int i = 0; i < TN; i++)
+    for (int u = 0; u < A_KB; u++) {
+      const int row = (wave + NW * u) * ROWS_PER_KB + lane / CHUNKS;
+      woff[u] = (uint32_t)(min(row, nlim) * a.ldw) + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
+    }
 #pragma unroll
-    for (int j = 0; j < TM; j++)
+    for (int u = 0; u < B_KB; u++) {
+      const int row = (wave + NW * u) * ROWS_PER_KB + lane / CHUNKS;
+      aoff[u] = (uint32_t)(min(row, mlim) * a.lda) + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
+    }
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
-  if constexpr (G128) {
+    for (int u = 0; u < SC_PER_WAVE; u++) {
+      const int q = wave + NW * u;
+      if (q < BN / 64) {
+        scbase[u] = a.sw + n0 * a.ldsw;
+        scoff[u] = (uint32_t)(min(q * 64 + lane, nlim) * a.ldsw);
+      } else if (q < SC_SLOTS) {
+        scbase[u] = a.sa + m0 * a.ldsa;
+        scoff[u] = (uint32_t)(min((q - BN / 64) * 64 + lane, mlim) * a.ldsa);
+      } else {
+        scbase[u] = a.sw + n0 * a.ldsw;
+        scoff[u] = 0;
+      }
+    }
+  };
+  auto issue_stage = [&](int kt, int buf) {
+    char* base = smem + SCR + buf * STAGE;
+    const uint8_t* wk = wbase + (int64_t)kt * BK;
+    const uint8_t* ak = abase + (int64_t)kt * BK;
+#pragma unroll
+    for (int u = 0; u < A_KB; u++) g2lds16(wk + woff[u], base + (wave + NW * u) * 1024);
+#pragma unroll
+    for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
+#pragma unroll
+    for (int u = 0; u < SC_PER_WAVE; u++)
+      g2lds4(scbase[u] + kt / STAGES_PER_GROUP + scoff[u], smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
+  };
+
+  const int nk = (int)(a.K / BK);
+  const int wrow_n = wn * TN * 32 + (lane & 31);  // this lane's A-fragment row within the weight tile
+  const int wrow_m = wm * TM * 32 + (lane & 31);  // and B-fragment row within the activation tile
+
+  // Fragments are read one MFMA slice ahead of the slice being multiplied (two register sets); the
+  // stage barrier sits between the last slice's reads and its MFMAs.
+  Frag fa[2][TN], fb[2][TM];
+  auto read_frags = [&](int set, const char* stage_base, int slice) {
+#pragma unroll
+    for (int i = 0; i < TN; i++) fa[set][i] = MF::template load<BK>(stage_base, wrow_n + i * 32, slice, lane);
+#pragma unroll
+    for (int j = 0; j < TM; j++) fb[set][j] = MF::template load<BK>(stage_base + A_BYTES, wrow_m + j * 32, slice, lane);
+  };
+
+  int64_t m0, n0;
+  tile_origin(t, m0, n0);
+  plan_loads(m0, n0, lane);
+  issue_stage(0, 0);
+
+  for (;;) {
+    // A per-tile copy of the lane id that the compiler cannot see through: the lane-dependent index
+    // math of the epilogue and of the next tile's load plan is recomputed per tile instead of being
+    // hoisted out of the tile loop and kept live (which would spill).
+    int tl = lane;
+    asm volatile("" : "+v"(tl));
+    // ---- main loop of tile (m0, n0); its stage 0 is in flight into buffer 0
+    Acc acc[TN][TM];                            // MFMA accumulators (whole K, or one group in g128 mode)
+    v16f facc[G128 ? TN : 1][G128 ? TM : 1];    // g128: fp32 running sum over groups
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
       for (int j = 0; j < TM; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) facc[i][j][r] = 0.0f;
-  }
-
-  const int nk = (int)(a.K / kBK);
-  const int wrow_n = wn * TN * 32 + (lane & 31);  // this lane's A-fragment row within the weight tile
-  const int wrow_m = wm * TM * 32 + (lane & 31);  // and B-fragment row within the activation tile
-
-  issue_stage(0, 0);
-  wait_vmem();
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) issue_stage(kt + 1, buf ^ 1);
-    const char* As = smem + buf * STAGE;
-    const char* Bs = As + A_BYTES;
+        for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
     if constexpr (G128) {
 #pragma unroll
       for (int i = 0; i < TN; i++)
 #pragma unroll
         for (int j = 0; j < TM; j++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+          for (int r = 0; r < 16; r++) facc[i][j][r] = 0.0f;
     }
+    // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging reads
+    // of the previous epilogue are done, so buffer 1 is free
+    wait_vmcnt<0>();
+    barrier();
+    if (1 < nk) issue_stage(1, 1);
+    read_frags(0, smem + SCR, 0);
+
+    int buf = 0;
+    for (int kt = 0; kt < nk; kt++) {
+      const char* stage = smem + SCR + buf * STAGE;
 #pragma unroll
-    for (int s = 0; s < SLICES; s++) {
-      Frag fa[TN], fb[TM];
+      for (int s = 0; s < SLICES; s++) {
+        const int cur = s & 1;
+        if (s + 1 < SLICES) {
+          read_frags(cur ^ 1, stage, s + 1);
+        } else if (kt + 1 < nk) {
+          // stage kt + 1 (the only loads in flight) has landed for this wave and its reads of stage kt
+          // are complete; the barrier publishes both facts, then stage kt + 2 may refill buffer `buf`
+          wait_vmcnt<0>();
+          __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+          barrier();
+          if (kt + 2 < nk) issue_stage(kt + 2, buf);
+          read_frags(cur ^ 1, smem + SCR + (buf ^ 1) * STAGE, 0);
+        }
 #pragma unroll
-      for (int i = 0; i < TN; i++) fa[i] = MF::load(As, wrow_n + i * 32, s, lane);
+        for (int i = 0; i < TN; i++)
 #pragma unroll
-      for (int j = 0; j < TM; j++) fb[j] = MF::load(Bs, wrow_m + j * 32, s, lane);
+          for (int j = 0; j < TM; j++) acc[i][j] = MF::run(fa[cur][i], fb[cur][j], acc[i][j]);
+      }
+      if constexpr (G128) {
+        if ((kt + 1) % STAGES_PER_GROUP == 0) {
+          const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
 #pragma unroll
-      for (int i = 0; i < TN; i++)
+          for (int j = 0; j < TM; j++) {
+            const float sam = sc[BN + wrow_m + j * 32];
 #pragma unroll
-        for (int j = 0; j < TM; j++) acc[i][j] = MF::run(fa[i], fb[j], acc[i][j]);
+            for (int i = 0; i < TN; i++) {
+#pragma unroll
+              for (int rr = 0; rr < 4; rr++) {
+                const float4 swv =
+                    *reinterpret_cast<const float4*>(sc + wn * TN * 32 + i * 32 + rr * 8 + (lane >> 5) * 4);
+                facc[i][j][rr * 4 + 0] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 0]) * sam, swv.x, facc[i][j][rr * 4 + 0]);
+                facc[i][j][rr * 4 + 1] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 1]) * sam, swv.y, facc[i][j][rr * 4 + 1]);
+                facc[i][j][rr * 4 + 2] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 2]) * sam, swv.z, facc[i][j][rr * 4 + 2]);
+                facc[i][j][rr * 4 + 3] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 3]) * sam, swv.w, facc[i][j][rr * 4 + 3]);
+              }
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < TN; i++)
+#pragma unroll
+            for (int j = 0; j < TM; j++)
+#pragma unroll
+              for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        }
+      }
+      buf ^= 1;
     }
-    if constexpr (G128) {
-      const float* sc = reinterpret_cast<const float*>(As + A_BYTES + B_BYTES);
+    // every wave is done reading the stage buffers (and the scale ring) of this tile
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    barrier();
+
+    // ---- next tile's first stage, then this tile's epilogue
+    const int64_t em0 = m0, en0 = n0;
+    t += nwx;
+    const bool more = t < t_end;
+    if (more) {
+      tile_origin(t, m0, n0);
+      plan_loads(m0, n0, tl);
+      issue_stage(0, 0);
+    }
+
+    // Tile-local coordinates (32-bit): lane holds token ml = wrow_m + 32 j and channels
+    // nl = wn*TN*32 + 32 i + 8 rr + 4 (lane >> 5) + q (q = 0..3) in register rr * 4 + q of tile (i, j);
+    // rows ml < mrem and channels nl < nrem exist.
+    const int mrem = (int)min<int64_t>(a.M - em0, BM), nrem = (int)min<int64_t>(a.N - en0, BN);
+    const int nloc = wn * TN * 32 + (tl >> 5) * 4;
+    const int erow_m = wm * TM * 32 + (tl & 31);
+    if constexpr (EPI == HN_EPI_ACC32) {
+      int32_t* obase = reinterpret_cast<int32_t*>(a.out) + em0 * a.ldo + en0;
 #pragma unroll
       for (int j = 0; j < TM; j++) {
-        const float sam = sc[BN + wrow_m + j * 32];
+        const int ml = erow_m + j * 32;
+        if (ml < mrem) {
+#pragma unroll
+          for (int i = 0; i < TN; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              const int nl = nloc + i * 32 + (r >> 2) * 8 + (r & 3);
+              if (nl < nrem) obase[(uint32_t)(ml * (int)a.ldo + nl)] = (int32_t)acc[i][j][r];
+            }
+        }
+      }
+    } else {
+      // Per-channel scale (per-token mode) and bias of the tile's BN channels, staged in LDS.
+      float* ep = reinterpret_cast<float*>(smem + EP_OFF);
+      for (int tt = tid; tt < BN; tt += NW * 64) {
+        const int64_t n = en0 + min(tt, nrem - 1);
+        ep[tt] = G128 ? 0.0f : a.sw[n * a.ldsw];
+        ep[BN + tt] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : 0.0f;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the ds_writes above have landed
+      barrier();
+      const bool has_bias = a.bias != nullptr;
+      const float* sabase = a.sa + em0 * a.ldsa;
+#pragma unroll
+      for (int j = 0; j < TM; j++) {
+        const int ml = erow_m + j * 32;
+        const bool m_ok = ml < mrem;
+        const float sam = G128 ? 0.0f : sabase[(uint32_t)(min(ml, mrem - 1) * (int)a.ldsa)];
+        // dequantize + bias (+ GELU) in place; the results overwrite the accumulator registers as fp32 bits
 #pragma unroll
         for (int i = 0; i < TN; i++) {
 #pragma unroll
           for (int rr = 0; rr < 4; rr++) {
-            const float4 swv =
-                *reinterpret_cast<const float4*>(sc + wn * TN * 32 + i * 32 + rr * 8 + (lane >> 5) * 4);
-            facc[i][j][rr * 4 + 0] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 0]) * sam, swv.x, facc[i][j][rr * 4 + 0]);
-            facc[i][j][rr * 4 + 1] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 1]) * sam, swv.y, facc[i][j][rr * 4 + 1]);
-            facc[i][j][rr * 4 + 2] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 2]) * sam, swv.z, facc[i][j][rr * 4 + 2]);
-            facc[i][j][rr * 4 + 3] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 3]) * sam, swv.w, facc[i][j][rr * 4 + 3]);
+            const float4 sw4 = *reinterpret_cast<const float4*>(ep + nloc + i * 32 + rr * 8);
+            const float4 b4 = *reinterpret_cast<const float4*>(ep + BN + nloc + i * 32 + rr * 8);
+            const float swq[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
+            const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const int r = rr * 4 + q;
+              float v;
+              if constexpr (G128) v = facc[i][j][r];
+              else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
+              if (has_bias) v = v + bq[q];
+              if constexpr (EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT) v = rbf16(gelu_tanh(rbf16(v)));
+              MF::put(acc[i][j], r, v);
+            }
           }
         }
-      }
-    }
-    wait_vmem();
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane holds token m = m0 + wrow_m + 32 j and channels n = n0 + wn*TN*32 + 32 i + 8 rr
-  //      + 4 (lane >> 5) + q (q = 0..3) in register rr * 4 + q of tile (i, j).
-  const int64_t nb = n0 + wn * TN * 32 + (lane >> 5) * 4;
-  if constexpr (EPI == HN_EPI_ACC32) {
+        if constexpr (EPI == HN_EPI_GELU_QUANT) {
+          // the wave's TN*32 = 128 channels are one group: lanes l and l^32 hold them for token m
+          float peak = 0.0f;
 #pragma unroll
-    for (int j = 0; j < TM; j++) {
-      const int64_t m = m0 + wrow_m + j * 32;
-      if (m < a.M) {
-        int32_t* o = reinterpret_cast<int32_t*>(a.out) + m * a.ldo;
+          for (int i = 0; i < TN; i++)
 #pragma unroll
-        for (int i = 0; i < TN; i++)
+            for (int r = 0; r < 16; r++) peak = __builtin_fmaxf(peak, __builtin_fabsf(MF::get(acc[i][j], r)));
+          peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));
+          const float gs = int8_scale(peak);
+          // the GELU outputs are bf16 values: the exact three-op quotient applies to the group (hn_common.h)
+          const bool fast = fast_group(peak);
+          const FastDiv<false> div(gs);
+          if (m_ok) {
+            int8_t* o = reinterpret_cast<int8_t*>(a.out) + em0 * a.ldo + en0;
 #pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int64_t n = nb + i * 32 + (r >> 2) * 8 + (r & 3);
-            if (n < a.N) o[n] = (int32_t)acc[i][j][r];
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int rr = 0; rr < 4; rr++) {
+                const int nl = nloc + i * 32 + rr * 8;
+                const float v0 = MF::get(acc[i][j], rr * 4 + 0), v1 = MF::get(acc[i][j], rr * 4 + 1);
+                const float v2 = MF::get(acc[i][j], rr * 4 + 2), v3 = MF::get(acc[i][j], rr * 4 + 3);
+                uint32_t w;
+                if (__builtin_expect(fast, 1))
+                  w = pack4_i8(round_half_away_i8_inrange(div(v0)), round_half_away_i8_inrange(div(v1)),
+                               round_half_away_i8_inrange(div(v2)), round_half_away_i8_inrange(div(v3)));
+                else
+                  w = pack4_i8(round_half_away_i8(v0 / gs), round_half_away_i8(v1 / gs), round_half_away_i8(v2 / gs),
+                               round_half_away_i8(v3 / gs));
+                if (nl < nrem) *reinterpret_cast<uint32_t*>(o + (uint32_t)(ml * (int)a.ldo + nl)) = w;
+              }
+            // N % 128 == 0, so the group is either wholly inside N or wholly past it
+            if (tl < 32 && wn * 128 < nrem) a.qs[(em0 + ml) * a.ldqs + (en0 + wn * 128) / 128] = gs;
           }
-      }
-    }
-    return;
-  } else {
-    // Per-channel scale (per-token mode) and bias of the block's BN channels, staged in the idle LDS.
-    float* ep = reinterpret_cast<float*>(smem + EP_OFF);
-    for (int t = tid; t < BN; t += NW * 64) {
-      const int64_t n = min(n0 + t, a.N - 1);
-      ep[t] = G128 ? 0.0f : a.sw[n * a.ldsw];
-      ep[BN + t] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : 0.0f;
-    }
-    __syncthreads();
-    const bool has_bias = a.bias != nullptr;
-    const int nloc = wn * TN * 32 + (lane >> 5) * 4;
-#pragma unroll
-    for (int j = 0; j < TM; j++) {
-      const int64_t m = m0 + wrow_m + j * 32;
-      const bool m_ok = m < a.M;
-      const float sam = G128 ? 0.0f : a.sa[(m_ok ? m : a.M - 1) * a.ldsa];
-      // dequantize + bias (+ GELU) in place; the results overwrite the accumulator registers as fp32 bits
-#pragma unroll
-      for (int i = 0; i < TN; i++) {
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-          const float4 sw4 = *reinterpret_cast<const float4*>(ep + nloc + i * 32 + rr * 8);
-          const float4 b4 = *reinterpret_cast<const float4*>(ep + BN + nloc + i * 32 + rr * 8);
-          const float swq[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
-          const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int r = rr * 4 + q;
-            float v;
-            if constexpr (G128) v = facc[i][j][r];
-            else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
-            if (has_bias) v = v + bq[q];
-            if constexpr (EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT) v = rbf16(gelu_tanh(rbf16(v)));
-            MF::put(acc[i][j], r, v);
-          }
-        }
-      }
-      if constexpr (EPI == HN_EPI_GELU_QUANT) {
-        // the wave's TN*32 = 128 channels are one group: lanes l and l^32 hold them for token m
-        float peak = 0.0f;
-#pragma unroll
-        for (int i = 0; i < TN; i++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) peak = __builtin_fmaxf(peak, __builtin_fabsf(MF::get(acc[i][j], r)));
-        peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));
-        const float gs = int8_scale(peak);
-        FastDiv div(gs);
-        if (m_ok) {
-          int8_t* o = reinterpret_cast<int8_t*>(a.out) + m * a.ldo;
+        } else if (STAGED && a.stage_store) {
+          // token row (tl & 31) of this wave's staging block, then a 16-byte-per-lane write-back of the
+          // block's 32 rows x TN*32 channels, non-temporal so the output stream does not evict the operand
+          // panels other tiles are still reading from L2
+          char* wst = smem + STG_OFF + wave * 32 * OPITCH;
+          char* ob = wst + (tl & 31) * OPITCH;
 #pragma unroll
           for (int i = 0; i < TN; i++)
 #pragma unroll
             for (int rr = 0; rr < 4; rr++) {
-              const int64_t n = nb + i * 32 + rr * 8;
-              const uint32_t w = pack4_i8(round_half_away_i8(div(MF::get(acc[i][j], rr * 4 + 0))), round_half_away_i8(div(MF::get(acc[i][j], rr * 4 + 1))),
-                                          round_half_away_i8(div(MF::get(acc[i][j], rr * 4 + 2))), round_half_away_i8(div(MF::get(acc[i][j], rr * 4 + 3))));
-              if (n < a.N) *reinterpret_cast<uint32_t*>(o + n) = w;
+              const int ocol = i * 32 + rr * 8 + (tl >> 5) * 4;
+              *reinterpret_cast<uint2*>(ob + ocol * 2) =
+                  make_uint2(cvt2_out<OUT_DT>(MF::get(acc[i][j], rr * 4 + 0), MF::get(acc[i][j], rr * 4 + 1)),
+                             cvt2_out<OUT_DT>(MF::get(acc[i][j], rr * 4 + 2), MF::get(acc[i][j], rr * 4 + 3)));
             }
-          // N % 128 == 0, so the group is either wholly inside N or wholly past it
-          if (lane < 32 && n0 + wn * 128 < a.N) a.qs[m * a.ldqs + (n0 + wn * 128) / 128] = gs;
-        }
-      } else if (STAGED && a.stage_store) {
-        // token row j*32 + (lane & 31) of this wave's staged sub-tile
-        char* ob = smem + wave * TM * 32 * OPITCH + (j * 32 + (lane & 31)) * OPITCH;
+          __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes have landed
+          __builtin_amdgcn_wave_barrier();
+          constexpr int LPR = TN * 32 * 2 / 16, RPI = 64 / LPR;  // lanes per token row, rows per instruction
+          uint16_t* obase = reinterpret_cast<uint16_t*>(a.out) + em0 * a.ldo + en0;
 #pragma unroll
-        for (int i = 0; i < TN; i++)
-#pragma unroll
-          for (int rr = 0; rr < 4; rr++) {
-            const int ocol = i * 32 + rr * 8 + (lane >> 5) * 4;
-            *reinterpret_cast<uint2*>(ob + ocol * 2) =
-                make_uint2(pack2_out<OUT_DT>(MF::get(acc[i][j], rr * 4 + 0), MF::get(acc[i][j], rr * 4 + 1)),
-                           pack2_out<OUT_DT>(MF::get(acc[i][j], rr * 4 + 2), MF::get(acc[i][j], rr * 4 + 3)));
+          for (int r0 = 0; r0 < 32; r0 += RPI) {
+            const int orow = r0 + tl / LPR, ocol = (tl % LPR) * 8;
+            const v4i v = *reinterpret_cast<const v4i*>(wst + orow * OPITCH + ocol * 2);
+            const int ml2 = wm * TM * 32 + j * 32 + orow, nl = wn * TN * 32 + ocol;
+            if (ml2 < mrem && nl < nrem)
+              __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(obase + (uint32_t)(ml2 * (int)a.ldo + nl)));
           }
-      } else if (m_ok) {
+        } else if (m_ok) {
 #pragma unroll
-        for (int i = 0; i < TN; i++)
+          for (int i = 0; i < TN; i++)
 #pragma unroll
-          for (int rr = 0; rr < 4; rr++) {
-            const int64_t n = nb + i * 32 + rr * 8;
-            const float v0 = MF::get(acc[i][j], rr * 4 + 0), v1 = MF::get(acc[i][j], rr * 4 + 1), v2 = MF::get(acc[i][j], rr * 4 + 2), v3 = MF::get(acc[i][j], rr * 4 + 3);
-            if constexpr (OUT_DT == HN_DTYPE_F32) {
-              float* o = reinterpret_cast<float*>(a.out) + m * a.ldo + n;
-              if (a.vec_store && n + 3 < a.N) {
-                *reinterpret_cast<float4*>(o) = make_float4(v0, v1, v2, v3);
+            for (int rr = 0; rr < 4; rr++) {
+              const int nl = nloc + i * 32 + rr * 8;
+              const uint32_t off = (uint32_t)(ml * (int)a.ldo + nl);
+              const float v0 = MF::get(acc[i][j], rr * 4 + 0), v1 = MF::get(acc[i][j], rr * 4 + 1), v2 = MF::get(acc[i][j], rr * 4 + 2), v3 = MF::get(acc[i][j], rr * 4 + 3);
+              if constexpr (OUT_DT == HN_DTYPE_F32) {
+                float* o = reinterpret_cast<float*>(a.out) + em0 * a.ldo + en0 + off;
+                if (a.vec_store && nl + 3 < nrem) {
+                  *reinterpret_cast<float4*>(o) = make_float4(v0, v1, v2, v3);
+                } else {
+                  if (nl < nrem) o[0] = v0;
+                  if (nl + 1 < nrem) o[1] = v1;
+                  if (nl + 2 < nrem) o[2] = v2;
+                  if (nl + 3 < nrem) o[3] = v3;
+                }
               } else {
-                if (n < a.N) o[0] = v0;
-                if (n + 1 < a.N) o[1] = v1;
-                if (n + 2 < a.N) o[2] = v2;
-                if (n + 3 < a.N) o[3] = v3;
-              }
-            } else {
-              uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + m * a.ldo + n;
-              const uint32_t lo = pack2_out<OUT_DT>(v0, v1), hi = pack2_out<OUT_DT>(v2, v3);
-              if (a.vec_store && n + 3 < a.N) {
-                *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
-              } else {
-                if (n < a.N) o[0] = (uint16_t)(lo & 0xffffu);
-                if (n + 1 < a.N) o[1] = (uint16_t)(lo >> 16);
-                if (n + 2 < a.N) o[2] = (uint16_t)(hi & 0xffffu);
-                if (n + 3 < a.N) o[3] = (uint16_t)(hi >> 16);
+                uint16_t* o = reinterpret_cast<uint16_t*>(a.out) + em0 * a.ldo + en0 + off;
+                const uint32_t lo = cvt2_out<OUT_DT>(v0, v1), hi = cvt2_out<OUT_DT>(v2, v3);
+                if (a.vec_store && nl + 3 < nrem) {
+                  *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+                } else {
+                  if (nl < nrem) o[0] = (uint16_t)(lo & 0xffffu);
+                  if (nl + 1 < nrem) o[1] = (uint16_t)(lo >> 16);
+                  if (nl + 2 < nrem) o[2] = (uint16_t)(hi & 0xffffu);
+                  if (nl + 3 < nrem) o[3] = (uint16_t)(hi >> 16);
+                }
               }
             }
-          }
-      }
-    }
-    if constexpr (STAGED) {
-      if (a.stage_store) {
-        // write-back: 16 bytes per lane along N, rows of TN*32 channels; non-temporal so the output stream
-        // does not evict the operand panels other tiles are still reading from L2
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes have landed
-        __builtin_amdgcn_wave_barrier();
-        const char* ob = smem + wave * TM * 32 * OPITCH;
-        constexpr int LPR = TN * 32 * 2 / 16, RPI = 64 / LPR;  // lanes per token row, rows per instruction
-#pragma unroll
-        for (int r0 = 0; r0 < TM * 32; r0 += RPI) {
-          const int orow = r0 + lane / LPR, ocol = (lane % LPR) * 8;
-          const v4i v = *reinterpret_cast<const v4i*>(ob + orow * OPITCH + ocol * 2);
-          const int64_t m = m0 + wm * TM * 32 + orow, n = n0 + wn * TN * 32 + ocol;
-          if (m < a.M && n < a.N)
-            __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.out) + m * a.ldo + n));
         }
       }
     }
+    if (!more) break;
   }
 }
 

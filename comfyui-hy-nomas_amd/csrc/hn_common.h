@@ -72,26 +72,52 @@ __device__ __forceinline__ uint32_t e4m3_encode(float f) {
 __device__ __forceinline__ float int8_scale(float peak) { return peak > 0.0f ? peak / 127.0f : 1.0f; }
 __device__ __forceinline__ float fp8_scale(float peak) { return (peak > 1e-12f ? peak : 1e-12f) / 448.0f; }
 
-// IEEE x / s for bf16-valued x and a scale derived from a bf16 absmax, in three VALU ops instead of a
-// full division: q0 = x * r, e = fma(-q0, s, x), q = fma(e, r, q0), r = 1 / s (correctly rounded).
+// The same scales for a peak with fast_group(peak): the quotient by the constant from its correctly
+// rounded reciprocal and one FMA correction, equal to the IEEE quotient for every bf16 peak >= 2^-80
+// (checked exhaustively on the CPU).
+__device__ __forceinline__ float div_by_const(float d, float c, float rc) {
+  const float q0 = d * rc;
+  const float e = __builtin_fmaf(-q0, c, d);
+  return __builtin_fmaf(e, rc, q0);
+}
+__device__ __forceinline__ float int8_scale_fast(float peak) { return div_by_const(peak, 127.0f, 1.0f / 127.0f); }
+__device__ __forceinline__ float fp8_scale_fast(float peak) {
+  return div_by_const(peak > 1e-12f ? peak : 1e-12f, 448.0f, 1.0f / 448.0f);
+}
+
+// IEEE x / s for bf16-valued x and a scale derived from a bf16 absmax, in three VALU ops per value instead
+// of a full division: q0 = x * r, e = fma(-q0, s, x), q = fma(e, r, q0), r = 1 / s (correctly rounded).
 // Checked exhaustively on the CPU for every bf16 absmax and every bf16 |x| <= absmax (int8: same fp32
-// bits; fp8: same e4m3 code) when r is finite and x == 0 or |x| >= 2^-100; other lanes divide.
+// bits; fp8: same e4m3 code) when r is finite and x == 0 or |x| >= 2^-100.  Callers use it for a whole
+// group when `fast_group(peak)` holds: then r is finite, and any 0 < |x| < 2^-100 gives |x / s| < 2^-11
+// on both paths, which is code 0 for int8 and for e4m3 (half its smallest subnormal is 2^-10).  Groups
+// with a smaller peak, and inputs that are not bf16 values, divide.  KEEP_SIGN restores the sign of a
+// zero quotient (-0 / s = -0 matters for the e4m3 sign bit, not for int8 codes).
+template <bool KEEP_SIGN>
 struct FastDiv {
   float s, r;
-  bool ok;
+  // r = RN(1 / scale): the hardware reciprocal (1 ulp) refined by one Newton step, which lands exactly on
+  // the correctly rounded reciprocal from anywhere within 2 ulp of it for every scale of a fast group
+  // (checked exhaustively on the CPU).
   __device__ __forceinline__ explicit FastDiv(float scale) : s(scale) {
-    r = 1.0f / scale;
-    ok = __builtin_isfinite(r);
+    const float r0 = __builtin_amdgcn_rcpf(scale);
+    r = __builtin_fmaf(__builtin_fmaf(-r0, scale, 1.0f), r0, r0);
   }
   __device__ __forceinline__ float operator()(float x) const {
-    float q0 = x * r;
-    float e = __builtin_fmaf(-q0, s, x);
-    float q = __builtin_copysignf(__builtin_fmaf(e, r, q0), x);
-    float ax = __builtin_fabsf(x);
-    if (__builtin_expect(!ok || (ax != 0.0f && ax < 0x1p-100f), 0)) q = x / s;
-    return q;
+    const float q0 = x * r;
+    const float e = __builtin_fmaf(-q0, s, x);
+    const float q = __builtin_fmaf(e, r, q0);
+    return KEEP_SIGN ? __builtin_copysignf(q, x) : q;
   }
 };
+
+__device__ __forceinline__ bool fast_group(float peak) { return peak >= 0x1p-80f; }
+
+// Code of y = x / scale with |x| <= the group's peak (so |y| <= 127 * (1 + 2^-22) and no clamp is needed):
+// round half away from zero as trunc(y + copysign(0.5, y)); NaN gives 0.
+__device__ __forceinline__ int round_half_away_i8_inrange(float y) {
+  return (int)(y + __builtin_copysignf(0.5f, y));
+}
 
 // Round half away from zero (kernels.py:35: floor(y + 0.5) / ceil(y - 0.5), each sum rounded in fp32),
 // clamp to +-127.  trunc(y + copysign(0.5, y)) equals that rule bit for bit: floor and trunc agree on
@@ -116,14 +142,67 @@ __device__ __forceinline__ int round_i8(float y) {
 
 // Pack four int8 codes (low byte first).
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)(d & 0xff) << 24);
+  const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);  // [a.b0, b.b0, 0, 0]
+  const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);                                // [ab.b0, ab.b1, cd.b0, cd.b1]
+}
+
+// fp32 pair -> packed bf16 pair, round to nearest even, with the hardware conversion (v_cvt_pk_bf16_f32).
+// It equals f32_to_bf16_bits for every non-NaN input; NaNs keep their sign and payload bits (quieted)
+// instead of becoming 0x7FC0, so callers use it where the values are known to be finite.
+__device__ __forceinline__ uint32_t bf16x2_finite(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
 }
 
 // ----------------------------------------------------------------------------------------------
 // cross-lane reductions (wave64)
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask, int width = 64) { return __shfl_xor(v, mask, width); }
+
+// DPP lane moves (VALU, no LDS round trip).  Controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140, row_bcast15 = 0x142, row_bcast31 = 0x143.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Max over the 16 lanes of each DPP row of non-negative values (compared as integers: the order of
+// non-negative floats, NaN above +inf).  Every lane of the row gets the result.
+__device__ __forceinline__ float row16_max_nonneg(float v) {
+  uint32_t u = __float_as_uint(v);
+  u = max(u, dpp_u<0xB1>(u));
+  u = max(u, dpp_u<0x4E>(u));
+  u = max(u, dpp_u<0x141>(u));
+  u = max(u, dpp_u<0x140>(u));
+  return __uint_as_float(u);
+}
+
+// Sum over the 64 lanes: butterflies within each row of 16, then rows 0..3 folded into lane 63 with row
+// broadcasts; the total is read from lane 63 (wave-uniform).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  v += dpp_f<0x142, 0xa>(v);  // rows 1, 3 += last lane of rows 0, 2
+  v += dpp_f<0x143, 0xc>(v);  // rows 2, 3 += last lane of row 1
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Max over the 64 lanes of non-negative values (as row16_max_nonneg), wave-uniform.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  uint32_t u = __float_as_uint(row16_max_nonneg(v));
+  u = max(u, dpp_u<0x142, 0xa>(u));
+  u = max(u, dpp_u<0x143, 0xc>(u));
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)u, 63));
+}
 
 // max over the 16 lanes of each DPP row
 __device__ __forceinline__ float row16_max(float v) {

@@ -31,23 +31,44 @@ struct Chunk8 {
   static constexpr int kElemBytes = DT == HN_DTYPE_F32 ? 4 : 2;
 };
 
-// Codes of 8 values with one scale; returns them packed in 8 bytes.
-template <int KIND, int ROUND>
-__device__ __forceinline__ uint2 encode8(const float* f, const FastDiv& div) {
+// Codes of 8 values with one scale; returns them packed in 8 bytes.  FAST: bf16-valued inputs in a group
+// with fast_group(peak) -- the three-op exact quotient, and (int8) no clamp since |x| <= peak.  Otherwise an
+// IEEE division and the clamped rounding.
+template <int KIND, int ROUND, bool FAST>
+__device__ __forceinline__ uint2 encode8(const float* f, float scale) {
   int c[8];
+  if constexpr (FAST) {
+    const FastDiv<KIND == HN_KIND_FP8> div(scale);
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    float y = div(f[i]);
-    if constexpr (KIND == HN_KIND_INT8) c[i] = round_i8<ROUND>(y);
-    else c[i] = (int)e4m3_encode(y);
+    for (int i = 0; i < 8; i++) {
+      const float y = div(f[i]);
+      if constexpr (KIND == HN_KIND_FP8) c[i] = (int)e4m3_encode(y);
+      else if constexpr (ROUND == HN_ROUND_HALF_EVEN) c[i] = (int)__builtin_rintf(y);
+      else c[i] = round_half_away_i8_inrange(y);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float y = f[i] / scale;
+      if constexpr (KIND == HN_KIND_FP8) c[i] = (int)e4m3_encode(y);
+      else c[i] = round_i8<ROUND>(y);
+    }
   }
   return make_uint2(pack4_i8(c[0], c[1], c[2], c[3]), pack4_i8(c[4], c[5], c[6], c[7]));
 }
 
-template <int KIND>
-__device__ __forceinline__ float group_scale(float peak) {
-  if constexpr (KIND == HN_KIND_INT8) return int8_scale(peak);
-  else return fp8_scale(peak);
+// Scale and codes of one group from its absmax `peak` (non-negative, NaN-free).  bf16 inputs in a group
+// with fast_group(peak) use the three-op quotients (hn_common.h); other groups and inputs divide.
+template <int DT, int KIND, int ROUND>
+__device__ __forceinline__ uint2 encode8_group(const float* f, float peak, float& scale) {
+  if constexpr (DT == HN_DTYPE_BF16) {
+    if (__builtin_expect(fast_group(peak), 1)) {
+      scale = KIND == HN_KIND_INT8 ? int8_scale_fast(peak) : fp8_scale_fast(peak);
+      return encode8<KIND, ROUND, true>(f, scale);
+    }
+  }
+  scale = KIND == HN_KIND_INT8 ? int8_scale(peak) : fp8_scale(peak);
+  return encode8<KIND, ROUND, false>(f, scale);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -83,10 +104,9 @@ __global__ __launch_bounds__(kG128Threads) void quant_g128_kernel(const char* __
     float peak = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i]));
-    peak = row16_max(peak);
-    const float sc = group_scale<KIND>(peak);
-    FastDiv div(sc);
-    uint2 codes = encode8<KIND, ROUND>(f, div);
+    peak = row16_max_nonneg(peak);  // per-lane maxima are NaN-free and >= 0
+    float sc;
+    const uint2 codes = encode8_group<DT, KIND, ROUND>(f, peak, sc);
     if (live[u]) {
       *reinterpret_cast<uint2*>(q + row[u] * ldq + grp[u] * 128 + lane16 * 8) = codes;
       if (lane16 == 0) s[row[u] * lds + grp[u]] = sc;
@@ -126,19 +146,18 @@ __global__ __launch_bounds__(kRowThreads) void quant_row_kernel(const char* __re
       for (int j = 0; j < 8; j++) peak = __builtin_fmaxf(peak, __builtin_fabsf(f[j]));
     }
   }
-  peak = wave_max(peak);
-  const float sc = group_scale<KIND>(peak);
-  FastDiv div(sc);
+  peak = wave_max_nonneg(peak);  // per-lane maxima are NaN-free and >= 0
+  float sc = 0.0f;
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     int64_t c = lane + 64 * i;
     if (c < nchunk) {
       float f[8];
       chunk[i].widen(f);
-      *reinterpret_cast<uint2*>(q + r * ldq + c * 8) = encode8<KIND, ROUND>(f, div);
+      *reinterpret_cast<uint2*>(q + r * ldq + c * 8) = encode8_group<DT, KIND, ROUND>(f, peak, sc);
     }
   }
-  if (lane == 0) s[r * lds] = sc;
+  if (lane == 0) s[r * lds] = sc;  // lane 0 always owns chunk 0 (K >= 128)
 }
 
 template <int DT, int KIND, int ROUND>

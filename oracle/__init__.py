@@ -71,6 +71,10 @@ def lib():
     l.hno_gelu_tanh.restype = ctypes.c_float
     l.hno_check_fast_division.argtypes = [ctypes.c_int, _i64, _i64]
     l.hno_check_fast_division.restype = ctypes.c_int64
+    l.hno_check_scale_division.argtypes = []
+    l.hno_check_scale_division.restype = ctypes.c_int64
+    l.hno_check_reciprocal_refinement.argtypes = []
+    l.hno_check_reciprocal_refinement.restype = ctypes.c_int64
     _lib = l
     return l
 

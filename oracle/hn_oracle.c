@@ -329,31 +329,99 @@ void hno_pixelumm_qk(const float* x, int64_t ldx, const float* wt, const float* 
     }
 }
 
-/* Division lemma used by the device quantizers: for a bf16 dividend x and a
- * scale s derived from a bf16 absmax, q0 = x * rcp(s); e = fma(-q0, s, x);
- * q1 = fma(e, rcp(s), q0) equals IEEE x / s whenever |x| >= 2^-100 and rcp(s) is
- * finite.  This routine checks it exhaustively over every positive finite bf16
- * peak and every bf16 |x| <= peak, comparing int8 quotients bit for bit (div
- * 127) or e4m3 codes (div 448).  Returns the number of mismatches. */
+/* Division lemma used by the device quantizers.  For a group whose bf16 absmax
+ * `peak` is at least 2^-80 the device computes every quotient x / s (x a bf16
+ * value, |x| <= peak) as q0 = x * rcp(s); e = fma(-q0, s, x); q1 = fma(e, rcp(s),
+ * q0), and an int8 code as trunc(q1 + copysign(0.5, q1)) without a clamp (or
+ * rint(q1) for half-to-even); smaller peaks divide.  This routine checks that
+ * rule exhaustively over every positive finite bf16 peak >= 2^-80 and every bf16
+ * |x| <= peak against the reference rule (IEEE x / s, then floor(q + .5) /
+ * ceil(q - .5) clamped to +-127, or rint + clamp), comparing int8 codes for both
+ * roundings (kind 0) or e4m3 codes (kind 1).  Returns the number of mismatches. */
+static int ref_code_half_away(float q) {
+    float t = q >= 0.0f ? floorf(q + 0.5f) : ceilf(q - 0.5f);
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    return (int)t;
+}
+static int ref_code_half_even(float q) {
+    float t = rintf(q);
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    return (int)t;
+}
 int64_t hno_check_fast_division(int fp8, int64_t peak_begin, int64_t peak_end) {
     int64_t bad = 0;
-    for (uint32_t pb = (uint32_t)peak_begin; pb < (uint32_t)peak_end; pb++) {
+    #pragma omp parallel for reduction(+:bad) schedule(dynamic, 64)
+    for (int64_t pbi = peak_begin; pbi < peak_end; pbi++) {
+        uint32_t pb = (uint32_t)pbi;
         float p = float_of(pb << 16);
+        if (!(p >= 0x1p-80f)) continue;  /* the device divides these groups */
         float s = fp8 ? fp8_scale(p) : int8_scale(p);
         float r = 1.0f / s;
-        int fast = isfinite(r);
+        if (!isfinite(r)) { bad++; continue; }
         for (uint32_t xb = 0; xb <= pb; xb++) {
-            float x = float_of(xb << 16);
-            float ref = x / s;
-            float got;
-            if (fast && fabsf(x) >= 0x1p-100f) {
+            for (int sign = 0; sign < 2; sign++) {
+                float x = float_of((xb << 16) | (sign ? 0x80000000u : 0u));
+                float ref = x / s;
                 float q0 = x * r;
                 float e = fmaf(-q0, s, x);
-                got = fmaf(e, r, q0);
-            } else {
-                got = x / s;
+                float got = fmaf(e, r, q0);
+                if (fp8) {
+                    got = copysignf(got, x);
+                    if (hno_e4m3_encode(got) != hno_e4m3_encode(ref)) bad++;
+                } else {
+                    int fast_away = (int)(got + copysignf(0.5f, got));
+                    int fast_even = (int)rintf(got);
+                    if (fast_away != ref_code_half_away(ref) || fast_even != ref_code_half_even(ref)) bad++;
+                }
             }
-            if (fp8 ? (hno_e4m3_encode(got) != hno_e4m3_encode(ref)) : (bits_of(got) != bits_of(ref))) bad++;
+        }
+    }
+    return bad;
+}
+
+/* The device's reciprocal of a group scale s (peaks >= 2^-80): r0 = v_rcp_f32(s), accurate to 1 ulp,
+ * refined by one Newton step r1 = fma(fma(-r0, s, 1), r0, r0).  For every bf16 peak >= 2^-80 and both
+ * scale kinds, this checks that every r0 within +-2 ulp of RN(1 / s) refines to exactly RN(1 / s), so
+ * the result does not depend on the hardware's approximation.  Returns the number of failures. */
+int64_t hno_check_reciprocal_refinement(void) {
+    int64_t bad = 0;
+    #pragma omp parallel for reduction(+:bad) schedule(static)
+    for (int64_t pbi = 1; pbi < 0x7F80; pbi++) {
+        float p = float_of((uint32_t)pbi << 16);
+        if (!(p >= 0x1p-80f)) continue;
+        for (int fp8 = 0; fp8 < 2; fp8++) {
+            float sc = fp8 ? fp8_scale(p) : int8_scale(p);
+            float want = 1.0f / sc;
+            uint32_t wb = bits_of(want);
+            for (int d = -2; d <= 2; d++) {
+                float r0 = float_of(wb + (uint32_t)d);
+                float e = fmaf(-r0, sc, 1.0f);
+                float r1 = fmaf(e, r0, r0);
+                if (bits_of(r1) != wb) bad++;
+            }
+        }
+    }
+    return bad;
+}
+
+/* The device's group scales for peaks >= 2^-80: peak / 127 (int8) and max(peak, 1e-12) / 448 (fp8)
+ * as q0 = d * rcp(c); e = fma(-q0, c, d); q1 = fma(e, rcp(c), q0) with rcp(c) the correctly rounded
+ * reciprocal of the constant.  Checks every positive finite bf16 peak >= 2^-80 against IEEE
+ * division; returns the number of mismatches. */
+int64_t hno_check_scale_division(void) {
+    int64_t bad = 0;
+    for (uint32_t pb = 1; pb < 0x7F80u; pb++) {
+        float p = float_of(pb << 16);
+        if (!(p >= 0x1p-80f)) continue;
+        for (int fp8 = 0; fp8 < 2; fp8++) {
+            float c = fp8 ? 448.0f : 127.0f;
+            float d = fp8 ? (p > 1e-12f ? p : 1e-12f) : p;
+            float r = 1.0f / c;
+            float q0 = d * r;
+            float e = fmaf(-q0, c, d);
+            float got = fmaf(e, r, q0);
+            float ref = fp8 ? fp8_scale(p) : int8_scale(p);
+            if (bits_of(got) != bits_of(ref)) bad++;
         }
     }
     return bad;

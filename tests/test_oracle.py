@@ -103,11 +103,24 @@ def test_quantize_zero_group_and_g128_weights():
 
 
 def test_fast_division_lemma_exhaustive():
-    """Every bf16 absmax and every bf16 |x| <= absmax: the device's reciprocal + FMA quotient equals IEEE
-    x / scale (int8: bit for bit; fp8: same e4m3 code)."""
+    """Every bf16 absmax >= 2^-80 and every bf16 x with |x| <= absmax, both signs: the device's reciprocal +
+    FMA quotient with unclamped rounding gives the same int8 codes (half away from zero and half to even) as
+    IEEE x / scale with the reference's clamped rounding, and the same e4m3 codes."""
     lib = oracle.lib()
     assert lib.hno_check_fast_division(0, 1, 0x7F80) == 0
     assert lib.hno_check_fast_division(1, 1, 0x7F80) == 0
+
+
+def test_reciprocal_refinement_exhaustive():
+    """The device's 1 / scale: any hardware reciprocal within 2 ulp, refined by one FMA Newton step, is the
+    correctly rounded reciprocal for every bf16 peak >= 2^-80 (int8 and fp8 scales)."""
+    assert oracle.lib().hno_check_reciprocal_refinement() == 0
+
+
+def test_fast_scale_division_exhaustive():
+    """The device's group scales peak / 127 and max(peak, 1e-12) / 448 from the reciprocal + FMA quotient
+    equal IEEE division for every bf16 peak >= 2^-80."""
+    assert oracle.lib().hno_check_scale_division() == 0
 
 
 # ------------------------------------------------------------------------------------------------
