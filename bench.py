@@ -37,6 +37,7 @@ HIDDEN = 3072
 # script, scaled by a plain-copy calibration (FETCH x2.0, WRITE x1.0); profiles/block_gemm_int8_per_token_M32768.md
 TRAFFIC_BYTES_PER_STEP = 7.26e9
 SLEEP_CYCLES = 2e8           # ~0.1 s of spin before each timed region
+WARM_S = 1.5                 # seconds of untimed GEMM work before the headline's timed region
 STACK = [("qkv", 3072, 9216), ("attn_out", 3072, 3072), ("ffn_up", 3072, 12288), ("ffn_down", 12288, 3072)]
 
 
@@ -59,13 +60,20 @@ def make_linear(n, k, gen, dev, groups):
     return w, sw.float(), bias
 
 
-def time_launches(fns, steps, warmup):
+def time_launches(fns, steps, warmup, warm_s=0.0):
     """Run the list of launches `steps` times; returns (ms per step, [avg ms per launch]) from HIP events
-    recorded on the current stream (the stream the kernels are launched on)."""
+    recorded on the current stream (the stream the kernels are launched on).  Before the timed region: `warmup`
+    untimed passes, then more untimed passes until `warm_s` seconds have elapsed, so the GPU clocks reach the
+    steady state of this work (they take about a second to settle under a matrix-core load)."""
     for _ in range(warmup):
         for f in fns:
             f()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < warm_s:
+        for f in fns:
+            f()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in fns]
           for _ in range(steps)]
@@ -86,7 +94,7 @@ def time_launches(fns, steps, warmup):
     return start.elapsed_time(end) / steps, per
 
 
-def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8"):
+def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", warm_s=WARM_S):
     """Headline stack.  Returns (ms/step, per-GEMM ms, total ops, [(name, K, N)])."""
     from hy_nomas import kernels
 
@@ -109,7 +117,7 @@ def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8"):
         keep.append((qa, sa, w, sw, bias))
         fns.append(lambda qa=qa, sa=sa, w=w, sw=sw, bias=bias: kernels.block_gemm(qa, sa, w, sw, bias, kind=kind))
         ops += 2 * M * n * k
-    ms, per = time_launches(fns, steps, warmup)
+    ms, per = time_launches(fns, steps, warmup, warm_s)
     del keep, fns
     torch.cuda.empty_cache()
     return ms, per, ops
@@ -166,6 +174,47 @@ def elementwise(dev, gen, steps, warmup):
     return out
 
 
+def dit_block(dev, gen, steps, warmup, per_token):
+    """One synthetic double-stream DiT block forward (hy_nomas/model.py:230-286) at hidden 3072, 24 heads x 128,
+    FFN 12288 GELU-tanh: 57344 image tokens (RoPE grid 14 x 64 x 64) + 256 text tokens, random int8 weights,
+    joint torch SDPA attention.  Returns {"block_ms", "attention_ms", "linear_path_ms", "linear_TOPS"}; the linear
+    path (every kernel of this package) is the block time minus the attention time of the same shapes."""
+    from hy_nomas import block
+
+    d, heads, mlp, lv, lt = HIDDEN, 24, 12288, 57344, 256
+
+    def linear(n, k):
+        qw = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+        sw = torch.rand(n, 1 if per_token else k // 128, generator=gen, device=dev) * 2e-3 + 5e-4
+        bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        return block.Int8Linear(qw, sw.float(), bias)
+
+    def stream():
+        lins = [linear(n, k) for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp))]
+        qn = (torch.rand(d // heads, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+        kn = (torch.rand(d // heads, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+        return block.DiTBlockInt8(*lins, qn, kn, heads, per_token=per_token)
+
+    blk = block.DoubleStreamBlockInt8(stream(), stream())
+    img = torch.randn(1, lv, d, generator=gen, device=dev).to(torch.bfloat16)
+    txt = torch.randn(1, lt, d, generator=gen, device=dev).to(torch.bfloat16)
+    mods = [[(torch.randn(1, d, generator=gen, device=dev) * 0.1).to(torch.bfloat16) for _ in range(6)]
+            for _ in range(2)]
+    rope = block.rope_freqs([16, 56, 56], 256, 14, 64, 64, device=dev)
+    with torch.no_grad():
+        ms, _ = time_launches([lambda: blk.forward(img, txt, mods[0], mods[1], rope)], steps, warmup)
+        q, k, v = (torch.randn(1, lv + lt, heads, d // heads, generator=gen, device=dev).to(torch.bfloat16)
+                   for _ in range(3))
+        att_ms, _ = time_launches([lambda: block.attention(q, k, v)], steps, warmup)
+    ops = 2 * (lv + lt) * sum(n * k for _, k, n in STACK)
+    lin_ms = ms - att_ms
+    del blk, img, txt, q, k, v
+    torch.cuda.empty_cache()
+    return {"block_ms": round(ms, 3), "attention_ms": round(att_ms, 3), "linear_path_ms": round(lin_ms, 3),
+            "linear_ops": ops, "linear_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
+            "activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
+
+
 def cpu_baseline(target_s=10.0):
     """The reference's CPU fallback (hy_nomas/ops.py:172-176: dequantize the g128 int8 weight to bf16, then
     F.linear) on a row sample of the four GEMMs; rows are scaled so the timed work is ~target_s."""
@@ -188,10 +237,11 @@ def cpu_baseline(target_s=10.0):
             oracle.dequant_linear(x, w, sw, bias)
         return time.perf_counter() - t0
 
-    rows = 64
-    dt = run(rows)                  # warm-up pass, also sizes the sample
-    rows = int(max(64, min(M, rows * target_s / max(dt, 1e-3) / 3)))
-    reps = 3 if dt * rows / 64 < target_s else 1
+    run(64)                          # thread pool and allocator warm-up
+    probe = 512
+    dt = run(probe)                  # sizes the sample: three passes of about target_s / 3 each
+    rows = int(max(64, min(M, probe * target_s / 3 / max(dt, 1e-3))))
+    reps = 3
     times = [run(rows) for _ in range(reps)]
     dt = sorted(times)[len(times) // 2]
     ops = sum(2 * rows * n * k for _, k, n in STACK)
@@ -207,6 +257,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--block-only", action="store_true", help="only the DiT block forward (both layouts)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 512 MiB five times (HBM counter calibration)")
     args = ap.parse_args()
@@ -227,6 +278,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(), "launches": 5}))
+        return
+
+    if args.block_only:
+        with torch.no_grad():
+            print(json.dumps({("per_token" if pt else "g128"): dit_block(dev, gen, 3, 1, pt) for pt in (True, False)}))
         return
 
     log("bench: int8 per-token x per-channel stack")
@@ -277,6 +333,13 @@ def main():
                                    "frac_fp8_peak": round(ops / (ms_f * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 3)}
         log("bench: elementwise")
         extra["elementwise"] = elementwise(dev, gen, max(10, args.steps), 3)
+        for pt in (True, False):
+            name = "dit_block_M57344_" + ("per_token" if pt else "g128")
+            log("bench: " + name)
+            try:
+                extra[name] = dit_block(dev, gen, 3, 1, pt)
+            except RuntimeError as e:  # e.g. no flash / memory-efficient SDPA kernel for this device
+                extra[name] = {"error": str(e)[:200]}
         result["extra"] = extra
     if not args.no_cpu:
         log("bench: cpu baseline")

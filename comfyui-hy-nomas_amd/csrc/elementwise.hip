@@ -50,7 +50,7 @@ __device__ __forceinline__ uint4 narrow8x(const float* f) {
 constexpr int kRowWaves = 8;
 constexpr int kRowThreads = kRowWaves * 64;
 
-template <int DT, int NORM, bool QUANT, int ROUND, int CPL, bool FULL>
+template <int DT, int NORM, bool QUANT, int ROUND, int CPL, bool FULL, bool PT>
 __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ shift,
                                                             const uint16_t* __restrict__ scale, int64_t L,
@@ -133,6 +133,51 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
   const float var = wave_sum_dpp(sq) / (float)D;
   const float rstd = 1.0f / __builtin_sqrtf(var + eps);
   const bool finite = fac_finite && __builtin_isfinite(mean) && __builtin_isfinite(rstd);
+  if constexpr (QUANT && PT) {
+    // one scale per token: y = rbf16(modulated norm) for the whole row, the row absmax, then the codes
+    static_assert(!QUANT || !PT || KEEP, "per-token adaLN quantization keeps the row in registers (D <= 4096)");
+    float peak = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const int c = lane + 64 * i;
+      if (has(i)) {
+        const float4 g0 = fac[c], g1 = fac[nchunk + c], h0 = fac[2 * nchunk + c], h1 = fac[3 * nchunk + c];
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float o = __builtin_fmaf(f[i][j] * rstd, g[j], h[j]);
+          f[i][j] = rbf16(o);
+          peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j]));  // NaN-free, >= 0
+        }
+      }
+    }
+    peak = wave_max_nonneg(peak);
+    const bool fast = fast_group(peak);
+    const float gs = fast ? int8_scale_fast(peak) : int8_scale(peak);
+    const FastDiv<false> div(gs);
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const int c = lane + 64 * i;
+      if (has(i)) {
+        int cd[8];
+        if (__builtin_expect(fast, 1)) {
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float v = div(f[i][j]);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(f[i][j] / gs);
+        }
+        *reinterpret_cast<uint2*>(q + r * D + c * 8) =
+            make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7]));
+      }
+    }
+    if (lane == 0) s[r] = gs;
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     const int c = lane + 64 * i;
@@ -190,7 +235,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
   }
 }
 
-template <int DT, int NORM, bool QUANT, int ROUND>
+template <int DT, int NORM, bool QUANT, int ROUND, bool PT>
 static int launch_adaln(const void* x, const void* shift, const void* scale, int64_t B, int64_t L, int64_t D,
                         float eps, void* y, int8_t* q, float* s, hipStream_t st) {
   const int64_t cpl = (D / 8 + 63) / 64;
@@ -204,27 +249,31 @@ static int launch_adaln(const void* x, const void* shift, const void* scale, int
 #define HN_CASE(N)                                                                                              \
   if (cpl <= N) {                                                                                               \
     if (D == 512 * N)                                                                                           \
-      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, true>), dim3(blocks), dim3(kRowThreads), lds, \
+      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, true, PT>), dim3(blocks), dim3(kRowThreads), lds, \
                          st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
                          (int)per_batch, (uint16_t*)y, q, s);                                                   \
     else                                                                                                        \
-      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, false>), dim3(blocks), dim3(kRowThreads), lds,\
+      hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, false, PT>), dim3(blocks), dim3(kRowThreads), lds,\
                          st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
                          (int)per_batch, (uint16_t*)y, q, s);                                                   \
     return HN_LAUNCH_CHECK("adaln_kernel");                                                                     \
   }
-  HN_CASE(1) HN_CASE(2) HN_CASE(3) HN_CASE(4) HN_CASE(5) HN_CASE(6) HN_CASE(8) HN_CASE(12) HN_CASE(16)
-  HN_CASE(24) HN_CASE(32)
+  HN_CASE(1) HN_CASE(2) HN_CASE(3) HN_CASE(4) HN_CASE(5) HN_CASE(6) HN_CASE(8)
+  if constexpr (!PT) {
+    HN_CASE(12) HN_CASE(16) HN_CASE(24) HN_CASE(32)
+  }
 #undef HN_CASE
-  set_error("adaln: D=%lld exceeds the supported 16384", (long long)D);
+  if (PT) set_error("adaln_quant: per-token scales support D <= 4096 (got %lld)", (long long)D);
+  else set_error("adaln: D=%lld exceeds the supported 16384", (long long)D);
   return HN_ERR_UNSUPPORTED;
 }
 
-template <int DT, bool QUANT, int ROUND>
+template <int DT, bool QUANT, int ROUND, bool PT = false>
 static int adaln_norm(int norm, const void* x, const void* shift, const void* scale, int64_t B, int64_t L,
                       int64_t D, float eps, void* y, int8_t* q, float* s, hipStream_t st) {
-  if (norm == HN_NORM_RMS) return launch_adaln<DT, HN_NORM_RMS, QUANT, ROUND>(x, shift, scale, B, L, D, eps, y, q, s, st);
-  return launch_adaln<DT, HN_NORM_LAYER, QUANT, ROUND>(x, shift, scale, B, L, D, eps, y, q, s, st);
+  if (norm == HN_NORM_RMS)
+    return launch_adaln<DT, HN_NORM_RMS, QUANT, ROUND, PT>(x, shift, scale, B, L, D, eps, y, q, s, st);
+  return launch_adaln<DT, HN_NORM_LAYER, QUANT, ROUND, PT>(x, shift, scale, B, L, D, eps, y, q, s, st);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -401,9 +450,11 @@ extern "C" int hn_adaln(const void* x, const void* shift, const void* scale, int
 }
 
 extern "C" int hn_adaln_quant(const void* x, const void* shift, const void* scale, int dtype, int64_t B, int64_t L,
-                              int64_t D, float eps, int norm, int rounding, int8_t* q, float* s, void* stream) {
+                              int64_t D, float eps, int norm, int rounding, int64_t group, int8_t* q, float* s,
+                              void* stream) {
   HN_REQUIRE(B >= 0 && L >= 0 && D > 0, "hn_adaln_quant: bad shape");
   HN_REQUIRE(D % 128 == 0, "hn_adaln_quant: D=%lld must be a multiple of 128", (long long)D);
+  HN_REQUIRE(group == 128 || group == D, "hn_adaln_quant: group must be 128 or D (got %lld)", (long long)group);
   HN_REQUIRE(norm == HN_NORM_LAYER || norm == HN_NORM_RMS, "hn_adaln_quant: bad norm %d", norm);
   HN_REQUIRE(rounding == HN_ROUND_HALF_AWAY || rounding == HN_ROUND_HALF_EVEN, "hn_adaln_quant: bad rounding");
   HN_REQUIRE(x && shift && scale && q && s, "hn_adaln_quant: null pointer");
@@ -411,16 +462,19 @@ extern "C" int hn_adaln_quant(const void* x, const void* shift, const void* scal
              "hn_adaln_quant: misaligned pointer");
   if (B * L == 0) return HN_OK;
   hipStream_t st = (hipStream_t)stream;
+  const bool pt = group == D && D != 128;  // one scale per token (a single group of 128 is the g128 layout)
+#define HN_AQ(DT, RD)                                                                                      \
+  return pt ? adaln_norm<DT, true, RD, true>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st)      \
+            : adaln_norm<DT, true, RD, false>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st)
   if (dtype == HN_DTYPE_BF16) {
-    if (rounding == HN_ROUND_HALF_EVEN)
-      return adaln_norm<HN_DTYPE_BF16, true, HN_ROUND_HALF_EVEN>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st);
-    return adaln_norm<HN_DTYPE_BF16, true, HN_ROUND_HALF_AWAY>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st);
+    if (rounding == HN_ROUND_HALF_EVEN) HN_AQ(HN_DTYPE_BF16, HN_ROUND_HALF_EVEN);
+    HN_AQ(HN_DTYPE_BF16, HN_ROUND_HALF_AWAY);
   }
   if (dtype == HN_DTYPE_F16) {
-    if (rounding == HN_ROUND_HALF_EVEN)
-      return adaln_norm<HN_DTYPE_F16, true, HN_ROUND_HALF_EVEN>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st);
-    return adaln_norm<HN_DTYPE_F16, true, HN_ROUND_HALF_AWAY>(norm, x, shift, scale, B, L, D, eps, nullptr, q, s, st);
+    if (rounding == HN_ROUND_HALF_EVEN) HN_AQ(HN_DTYPE_F16, HN_ROUND_HALF_EVEN);
+    HN_AQ(HN_DTYPE_F16, HN_ROUND_HALF_AWAY);
   }
+#undef HN_AQ
   set_error("hn_adaln_quant: unsupported dtype %d", dtype);
   return HN_ERR_UNSUPPORTED;
 }

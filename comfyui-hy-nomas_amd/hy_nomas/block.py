@@ -79,17 +79,24 @@ class Int8Linear:
 class DiTBlockInt8:
     """One stream of the double-stream block on the int8 path (hy_nomas/model.py:246-286).
 
-    qkv, proj, fc1, fc2: Int8Linear.  q_norm_w / k_norm_w: [head_dim] bf16."""
+    qkv, proj, fc1, fc2: Int8Linear.  q_norm_w / k_norm_w: [head_dim] bf16.
+    per_token=False: the reference's layout -- activations quantized per token and 128 channels (adaLN
+    quantization, the FFN-up GELU + requantization epilogue), weights per 128-channel group or per channel.
+    per_token=True: one scale per token for every activation and per-channel weights ([N, 1] scales), so every
+    GEMM accumulates the whole K in int32; FFN-up then writes bf16 GELU outputs that are quantized per token
+    (a per-token requantization needs the whole row, which no GEMM tile holds)."""
 
-    def __init__(self, qkv, proj, fc1, fc2, q_norm_w, k_norm_w, heads):
+    def __init__(self, qkv, proj, fc1, fc2, q_norm_w, k_norm_w, heads, per_token=False):
         self.qkv, self.proj, self.fc1, self.fc2 = qkv, proj, fc1, fc2
         self.q_norm_w, self.k_norm_w = q_norm_w, k_norm_w
         self.heads = heads
+        self.per_token = per_token
+        self.group = None if per_token else kernels.GROUP
 
     def attention_inputs(self, x, shift1, scale1, rope=None):
         """adaLN + int8 quantization shared by q/k/v -> one QKV GEMM -> QK-norm (+RoPE).  x [B, L, D]."""
         b, n, d = x.shape
-        qa, sa = kernels.adaln_quant(x, shift1, scale1)
+        qa, sa = kernels.adaln_quant(x, shift1, scale1, group=self.group)
         qkv = kernels.block_gemm(qa, sa, self.qkv.qw, self.qkv.sw, self.qkv.bias, out_dtype=x.dtype)
         qkv = qkv.view(b, n, 3, self.heads, d // self.heads)
         q = fused.qk_norm_rope(qkv[:, :, 0], self.q_norm_w, rope)
@@ -100,8 +107,13 @@ class DiTBlockInt8:
     def post(self, x, attn, gate1, shift2, scale2, gate2):
         """Out-projection + gated residual, then the MLP half with its gated residual.  attn [B, L, D]."""
         x = fused.gated_residual(x, kernels.block_linear(attn, self.proj.qw, self.proj.sw, self.proj.bias), gate1)
-        qa, sa = kernels.adaln_quant(x, shift2, scale2)
-        qh, sh = kernels.block_gemm(qa, sa, self.fc1.qw, self.fc1.sw, self.fc1.bias, epilogue="gelu_quant")
+        qa, sa = kernels.adaln_quant(x, shift2, scale2, group=self.group)
+        if self.per_token:
+            g = kernels.block_gemm(qa, sa, self.fc1.qw, self.fc1.sw, self.fc1.bias, out_dtype=x.dtype, epilogue="gelu")
+            qh, sh = kernels.quantize_activations(g, group=None)
+            del g
+        else:
+            qh, sh = kernels.block_gemm(qa, sa, self.fc1.qw, self.fc1.sw, self.fc1.bias, epilogue="gelu_quant")
         h = kernels.block_gemm(qh, sh, self.fc2.qw, self.fc2.sw, self.fc2.bias, out_dtype=x.dtype)
         return fused.gated_residual(x, h.view_as(x), gate2)
 
@@ -109,7 +121,86 @@ class DiTBlockInt8:
         """Self-attention over this stream only (torch SDPA, unchanged), then `post`."""
         shift1, scale1, gate1, shift2, scale2, gate2 = mods
         q, k, v = self.attention_inputs(x, shift1, scale1, rope)
-        attn = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
-                                              v.transpose(1, 2).contiguous())
-        attn = attn.transpose(1, 2).reshape(x.shape)
+        attn = attention(q, k, v).reshape(x.shape)
         return self.post(x, attn, gate1, shift2, scale2, gate2)
+
+
+def attention(q, k, v):
+    """Joint softmax attention over the token axis with torch SDPA: q, k, v [B, L, H, D] -> [B, L, H, D].
+
+    The operands are made contiguous in [B, H, L, D] first (torch's batched bf16 products misbehave on
+    transposed views), and only the flash / memory-efficient kernels are allowed: at video lengths the
+    math fallback would materialize an [L, L] score matrix per head, so an unsupported case raises."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        out = F.scaled_dot_product_attention(qh, kh, vh)
+    return out.transpose(1, 2)
+
+
+class DoubleStreamBlockInt8:
+    """The double-stream DiT block on the int8 path (hy_nomas/model.py:230-286): image and text streams with
+    their own weights and modulations, one joint attention over the concatenated tokens (image first), then
+    each stream's out-projection, gated residuals and MLP.  The image stream gets RoPE; the text stream none.
+
+    img / txt: DiTBlockInt8 halves.  forward(img, txt, img_mods, txt_mods, rope) -> (img, txt)."""
+
+    def __init__(self, img, txt):
+        self.img, self.txt = img, txt
+
+    def forward(self, img, txt, img_mods, txt_mods, rope=None):
+        shift1, scale1, gate1, shift2, scale2, gate2 = img_mods
+        tshift1, tscale1, tgate1, tshift2, tscale2, tgate2 = txt_mods
+        iq, ik, iv = self.img.attention_inputs(img, shift1, scale1, rope)
+        tq, tk, tv = self.txt.attention_inputs(txt, tshift1, tscale1, None)
+        q = torch.cat([iq, tq], dim=1)
+        k = torch.cat([ik, tk], dim=1)
+        v = torch.cat([iv, tv], dim=1)
+        del iq, ik, iv, tq, tk, tv
+        attn = attention(q, k, v)
+        del q, k, v
+        b, lv = img.shape[0], img.shape[1]
+        attn = attn.reshape(b, attn.shape[1], -1)
+        img = self.img.post(img, attn[:, :lv], gate1, shift2, scale2, gate2)
+        txt = self.txt.post(txt, attn[:, lv:], tgate1, tshift2, tscale2, tgate2)
+        return img, txt
+
+
+def reference_double_stream(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope=None, eps=1e-6):
+    """The same double-stream block in float32 torch arithmetic with dequantized weights and unquantized
+    activations (the reference's exact-matmul path, hy_nomas/model.py:246-286 with ops.py:172-176); tensors may
+    live on any device.  Returns (img, txt) float32."""
+    def lin(x, l):
+        w = l.qw.float() * l.sw.float().repeat_interleave(l.qw.shape[1] // l.sw.shape[1], dim=1)
+        return F.linear(x, w, None if l.bias is None else l.bias.float())
+
+    def qkv(blk, x, mods, rope):
+        shift1, scale1 = mods[0].float(), mods[1].float()
+        xm = modulate(layer_norm(x, eps), shift1, scale1).to(torch.bfloat16).float()
+        b, n, d = x.shape
+        t = lin(xm, blk.qkv).view(b, n, 3, blk.heads, d // blk.heads)
+        q, k, v = t[:, :, 0], t[:, :, 1], t[:, :, 2]
+
+        def rms(z, w):
+            return z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+        q, k = rms(q, blk.q_norm_w), rms(k, blk.k_norm_w)
+        if rope is not None:
+            q, k = apply_rope(q, *rope), apply_rope(k, *rope)
+        return q, k, v
+
+    def post(blk, x, attn, mods):
+        gate1, shift2, scale2, gate2 = (m.float() for m in mods[2:])
+        x = x + lin(attn, blk.proj) * gate1.unsqueeze(1)
+        h = lin(modulate(layer_norm(x, eps), shift2, scale2), blk.fc1)
+        h = F.gelu(h, approximate="tanh")
+        return x + lin(h, blk.fc2) * gate2.unsqueeze(1)
+
+    img, txt = img.float(), txt.float()
+    iq, ik, iv = qkv(img_blk, img, img_mods, rope)
+    tq, tk, tv = qkv(txt_blk, txt, txt_mods, None)
+    q, k, v = (torch.cat(p, dim=1).transpose(1, 2) for p in ((iq, tq), (ik, tk), (iv, tv)))
+    att = torch.softmax(q @ k.transpose(-1, -2) / q.shape[-1] ** 0.5, dim=-1) @ v
+    att = att.transpose(1, 2).reshape(img.shape[0], -1, img.shape[2])
+    lv = img.shape[1]
+    return post(img_blk, img, att[:, :lv], img_mods), post(txt_blk, txt, att[:, lv:], txt_mods)

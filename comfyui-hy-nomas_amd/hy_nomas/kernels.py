@@ -110,21 +110,23 @@ def block_gemm_acc32(qa, qw):
     return out
 
 
-def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away"):
+def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away", group=GROUP):
     """x [B, L, D] bf16, shift/scale [B, D] -> int8 codes [B * L, D] and scales [B * L, D / 128] of the
     modulated LayerNorm (hy_nomas/kernels.py:198-207).  Any D that is a multiple of 128 (e.g. 3072);
-    `norm="rms"` uses RMSNorm instead of LayerNorm."""
+    `norm="rms"` uses RMSNorm instead of LayerNorm; `group=None` gives one scale per token ([B * L, 1],
+    D <= 4096)."""
     _lib.require_device(x, shift, scale)
     b, l, d = x.shape
+    g = d if group is None else group
     x = x.contiguous()
     shift = shift.to(x.dtype).contiguous()
     scale = scale.to(x.dtype).contiguous()
     q = torch.empty((b * l, d), device=x.device, dtype=torch.int8)
-    s = torch.empty((b * l, d // GROUP), device=x.device, dtype=torch.float32)
+    s = torch.empty((b * l, d // g), device=x.device, dtype=torch.float32)
     if b * l == 0:
         return q, s
     _lib.call("hn_adaln_quant", x.data_ptr(), shift.data_ptr(), scale.data_ptr(), _lib.dtype_code(x), b, l, d, eps,
-              _lib.NORM[norm], _lib.ROUND[rounding], q.data_ptr(), s.data_ptr(), _lib.stream(x))
+              _lib.NORM[norm], _lib.ROUND[rounding], g, q.data_ptr(), s.data_ptr(), _lib.stream(x))
     return q, s
 
 

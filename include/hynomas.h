@@ -87,12 +87,14 @@ int hn_adaln(const void* x, const void* shift, const void* scale, int dtype, int
              float eps, int norm, void* y, void* stream);
 
 /*
- * LayerNorm (or RMSNorm) + modulate + int8 quantization per 128 channels.  Replaces kernels.adaln_quant /
- * _adaln_quant_kernel (hy_nomas/kernels.py:173-207).  D % 128 == 0 (any multiple, e.g. 3072).
- *   q [B * L, D] int8, s [B * L, D / 128] fp32 of bf16(norm(x) * bf16(1 + scale) + shift).
+ * LayerNorm (or RMSNorm) + modulate + int8 quantization.  Replaces kernels.adaln_quant / _adaln_quant_kernel
+ * (hy_nomas/kernels.py:173-207).  D % 128 == 0 (any multiple, e.g. 3072).
+ *   q [B * L, D] int8 codes of bf16(norm(x) * bf16(1 + scale) + shift), scales s fp32:
+ *   group = 128 (the reference): s [B * L, D / 128], one scale per token and 128 channels;
+ *   group = D (per-token extension, D <= 4096): s [B * L, 1].
  */
 int hn_adaln_quant(const void* x, const void* shift, const void* scale, int dtype, int64_t B, int64_t L,
-                   int64_t D, float eps, int norm, int rounding, int8_t* q, float* s, void* stream);
+                   int64_t D, float eps, int norm, int rounding, int64_t group, int8_t* q, float* s, void* stream);
 
 /*
  * Gated residual.  Replaces fused.gated_residual / _gated_residual_kernel (hy_nomas/fused.py:108-128).

@@ -48,7 +48,7 @@ def test_argument_validation_without_a_gpu():
     rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, None, 0, 4, 8, 256, 64, 0, 0, None, 0, 8, None, 0,
                          None)   # group 64
     assert rc == 1 and b"group" in l.hn_last_error()
-    rc = l.hn_adaln_quant(None, None, None, 0, 1, 4, 200, 1e-6, 0, 0, None, None, None)   # D % 128 != 0
+    rc = l.hn_adaln_quant(None, None, None, 0, 1, 4, 200, 1e-6, 0, 0, 128, None, None, None)   # D % 128 != 0
     assert rc == 1 and b"multiple of 128" in l.hn_last_error()
     rc = l.hn_qk_norm_rope(None, 96, None, None, None, 1, 1, 1, 96, 1e-6, None, None)   # head dim 96
     assert rc == 1

@@ -142,3 +142,22 @@ def test_pixelumm_qk(dev):
     ref = bf(torch.from_numpy(oracle.pixelumm_qk(x, wt, whw, cos, sin)))
     assert (got != ref).float().mean().item() < 1e-2
     assert ((got.float() - ref.float()).norm() / ref.float().norm()).item() < 1e-3
+
+
+@pytest.mark.parametrize("b,l,d", [(1, 300, 3072), (2, 77, 2048), (1, 5, 128)])
+def test_adaln_quant_per_token(dev, b, l, d):
+    """The per-token extension: one scale per row of the modulated norm, the oracle's per-token quantization of
+    the oracle's rbf16 adaLN output (codes to the reference test's 1e-3 mismatch, scales to 1e-3)."""
+    from hy_nomas import kernels
+
+    print(f"adaln_quant per-token b={b} l={l} d={d}", flush=True)
+    g = seeded(l + d + 7)
+    x = bf(torch.randn(b, l, d, generator=g) * 3)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), group=None)
+    assert tuple(s.shape) == (b * l, 1)
+    _, _, y = oracle.adaln(x, shift, scale, quant=True)
+    q_ref, s_ref = oracle.quantize(y, d)
+    assert (q.cpu().numpy() != q_ref).mean() < 1e-3
+    assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-3)
