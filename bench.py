@@ -62,9 +62,11 @@ def make_linear(n, k, gen, dev, groups):
 
 def time_launches(fns, steps, warmup, warm_s=0.0):
     """Run the list of launches `steps` times; returns (ms per step, [avg ms per launch]) from HIP events
-    recorded on the current stream (the stream the kernels are launched on).  Before the timed region: `warmup`
-    untimed passes, then more untimed passes until `warm_s` seconds have elapsed, so the GPU clocks reach the
-    steady state of this work (they take about a second to settle under a matrix-core load)."""
+    recorded on the current stream (the stream the kernels are launched on): the step time from one event
+    pair around all steps, the per-launch averages from a second pass with an event pair around every launch.
+    Before the timed region: `warmup` untimed passes, then more untimed passes until `warm_s` seconds have
+    elapsed, so the GPU clocks reach the steady state of this work (they take about a second to settle under
+    a matrix-core load)."""
     for _ in range(warmup):
         for f in fns:
             f()
@@ -84,14 +86,21 @@ def time_launches(fns, steps, warmup, warm_s=0.0):
     torch.cuda._sleep(int(SLEEP_CYCLES))
     start.record(stream)
     for s in range(steps):
+        for f in fns:
+            f()
+    end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end) / steps
+    # a second pass with an event pair around every launch, for the per-launch averages
+    torch.cuda._sleep(int(SLEEP_CYCLES))
+    for s in range(steps):
         for i, f in enumerate(fns):
             ev[s][i][0].record(stream)
             f()
             ev[s][i][1].record(stream)
-    end.record(stream)
     torch.cuda.synchronize()
     per = [sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(steps)) / steps for i in range(len(fns))]
-    return start.elapsed_time(end) / steps, per
+    return total_ms, per
 
 
 def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", warm_s=WARM_S):
@@ -215,7 +224,7 @@ def dit_block(dev, gen, steps, warmup, per_token):
             "activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
 
 
-def cpu_baseline(target_s=10.0):
+def cpu_baseline(target_s=20.0):
     """The reference's CPU fallback (hy_nomas/ops.py:172-176: dequantize the g128 int8 weight to bf16, then
     F.linear) on a row sample of the four GEMMs; rows are scaled so the timed work is ~target_s."""
     import oracle

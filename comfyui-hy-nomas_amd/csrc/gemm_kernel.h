@@ -248,26 +248,29 @@ void block_gemm_kernel(const GemmArgs a) {
   auto plan_loads = [&](int64_t m0, int64_t n0, int lane) {
     wbase = a.qw + n0 * a.ldw;
     abase = a.qa + m0 * a.lda;
-    const int nlim = (int)min<int64_t>(a.N - 1 - n0, BN - 1), mlim = (int)min<int64_t>(a.M - 1 - m0, BM - 1);
+    // last valid row of each operand tile (tiles past the edge re-read it)
+    const int64_t nrem1 = a.N - 1 - n0, mrem1 = a.M - 1 - m0;
+    const int nlim = nrem1 < BN - 1 ? (int)nrem1 : BN - 1, mlim = mrem1 < BM - 1 ? (int)mrem1 : BM - 1;
+    const uint32_t ldw = (uint32_t)a.ldw, lda = (uint32_t)a.lda;
 #pragma unroll
     for (int u = 0; u < A_KB; u++) {
       const int row = (wave + NW * u) * ROWS_PER_KB + lane / CHUNKS;
-      woff[u] = (uint32_t)(min(row, nlim) * a.ldw) + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
+      woff[u] = (uint32_t)min(row, nlim) * ldw + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
     }
 #pragma unroll
     for (int u = 0; u < B_KB; u++) {
       const int row = (wave + NW * u) * ROWS_PER_KB + lane / CHUNKS;
-      aoff[u] = (uint32_t)(min(row, mlim) * a.lda) + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
+      aoff[u] = (uint32_t)min(row, mlim) * lda + (swz_chunk<BK>(row, lane % CHUNKS) << 4);
     }
 #pragma unroll
     for (int u = 0; u < SC_PER_WAVE; u++) {
       const int q = wave + NW * u;
       if (q < BN / 64) {
         scbase[u] = a.sw + n0 * a.ldsw;
-        scoff[u] = (uint32_t)(min(q * 64 + lane, nlim) * a.ldsw);
+        scoff[u] = (uint32_t)min(q * 64 + lane, nlim) * (uint32_t)a.ldsw;
       } else if (q < SC_SLOTS) {
         scbase[u] = a.sa + m0 * a.ldsa;
-        scoff[u] = (uint32_t)(min((q - BN / 64) * 64 + lane, mlim) * a.ldsa);
+        scoff[u] = (uint32_t)min((q - BN / 64) * 64 + lane, mlim) * (uint32_t)a.ldsa;
       } else {
         scbase[u] = a.sw + n0 * a.ldsw;
         scoff[u] = 0;
@@ -404,7 +407,8 @@ void block_gemm_kernel(const GemmArgs a) {
     // Tile-local coordinates (32-bit): lane holds token ml = wrow_m + 32 j and channels
     // nl = wn*TN*32 + 32 i + 8 rr + 4 (lane >> 5) + q (q = 0..3) in register rr * 4 + q of tile (i, j);
     // rows ml < mrem and channels nl < nrem exist.
-    const int mrem = (int)min<int64_t>(a.M - em0, BM), nrem = (int)min<int64_t>(a.N - en0, BN);
+    const int64_t mleft = a.M - em0, nleft = a.N - en0;
+    const int mrem = mleft < BM ? (int)mleft : BM, nrem = nleft < BN ? (int)nleft : BN;
     const int nloc = wn * TN * 32 + (tl >> 5) * 4;
     const int erow_m = wm * TM * 32 + (tl & 31);
     if constexpr (EPI == HN_EPI_ACC32) {
@@ -555,6 +559,10 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     }
     if (!more) break;
+    // the next tile's load offsets again (recomputed rather than kept live across the epilogue)
+    int tl2 = lane;
+    asm volatile("" : "+v"(tl2));
+    plan_loads(m0, n0, tl2);
   }
 }
 
