@@ -119,7 +119,7 @@ def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", war
             qa, sa = kernels.quantize_activations(x, "fp8", 128)
             wf = torch.randn(n, k, generator=gen, device=dev) * 0.02
             w, sblk = pixelumm.quantize_fp8_block(wf)
-            sw = sblk.repeat_interleave(128, 0).contiguous()
+            sw = sblk   # [N/128, K/128] block scales, read directly by the GEMM
             bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
             del wf
         del x

@@ -20,7 +20,7 @@ static int cu_count() {
   return cached[dev];
 }
 
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS>
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK = false>
 static int launch_cfg(GemmArgs& a, hipStream_t st) {
   constexpr int BN = WN * TN * 32, BM = WM * TM * 32;
   const int64_t tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
@@ -31,7 +31,7 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
   a.tiles_m = (int)tm;
   a.tiles_n = (int)tn;
   const int64_t grid = tm * tn < cu_count() ? tm * tn : cu_count();
-  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS, WBLK>), dim3((unsigned)grid),
                      dim3(WN * WM * 64), 0, st, a);
   return HN_LAUNCH_CHECK("block_gemm_kernel");
 }
@@ -40,6 +40,7 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
 // 128-byte K stages in two LDS buffers.
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
+  if (g128 && a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2, true>(a, st);
   if (g128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
   return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
 }
@@ -70,7 +71,7 @@ static int launch_kind(GemmArgs& a, bool g128, int epilogue, int out_dtype, hipS
 }  // namespace hn
 
 extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
-                             const float* sw, int64_t ldsw, const void* bias, int bias_dtype, int64_t M, int64_t N,
+                             const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t M, int64_t N,
                              int64_t K, int64_t group, int kind, int epilogue, void* out, int out_dtype, int64_t ldo,
                              float* qs, int64_t ldqs, void* stream) {
   using namespace hn;
@@ -90,6 +91,8 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   HN_REQUIRE(lda % 16 == 0 && ldw % 16 == 0, "hn_block_gemm: code row strides must be multiples of 16 bytes");
   HN_REQUIRE(lda < (1 << 22) && ldw < (1 << 22) && ldsa < (1 << 22) && ldsw < (1 << 22) && ldo < (1 << 22),
              "hn_block_gemm: row strides must be below 2^22 elements");
+  HN_REQUIRE(sw_rows == 1 || (sw_rows == 128 && group == 128 && epilogue != HN_EPI_ACC32),
+             "hn_block_gemm: sw_rows must be 1, or 128 with group 128 (got %lld)", (long long)sw_rows);
   HN_REQUIRE(qa && qw && out, "hn_block_gemm: null pointer");
   HN_REQUIRE(((uintptr_t)qa & 15) == 0 && ((uintptr_t)qw & 15) == 0, "hn_block_gemm: codes must be 16-byte aligned");
   if (epilogue != HN_EPI_ACC32) {
@@ -99,7 +102,7 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   if (M == 0) return HN_OK;
   GemmArgs a{};
   a.qa = (const uint8_t*)qa; a.lda = lda; a.sa = sa; a.ldsa = ldsa;
-  a.qw = (const uint8_t*)qw; a.ldw = ldw; a.sw = sw; a.ldsw = ldsw;
+  a.qw = (const uint8_t*)qw; a.ldw = ldw; a.sw = sw; a.ldsw = ldsw; a.sw_rows = (int)sw_rows;
   a.bias = bias; a.bias_dtype = bias_dtype;
   a.M = M; a.N = N; a.K = K;
   a.out = out; a.ldo = ldo; a.qs = qs; a.ldqs = ldqs;
@@ -107,8 +110,8 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   a.vec_store = (N % 4 == 0) && (ldo % 4 == 0) && ((((uintptr_t)out) & (4 * esz - 1)) == 0);
   a.stage_store = esz == 2 && (N % 8 == 0) && (ldo % 8 == 0) && ((((uintptr_t)out) & 15) == 0);
   hipStream_t st = (hipStream_t)stream;
-  // per-token mode also serves a single-group K == 128 problem
-  const bool g128 = group == 128 && K != 128;
+  // per-token mode also serves a single-group K == 128 problem with one scale row per channel
+  const bool g128 = group == 128 && (K != 128 || sw_rows == 128);
   if (epilogue == HN_EPI_ACC32) return launch_group<HN_KIND_INT8, HN_EPI_ACC32, HN_DTYPE_BF16>(a, false, st);
   if (kind == HN_KIND_INT8) return launch_kind<HN_KIND_INT8>(a, g128, epilogue, out_dtype, st);
   return launch_kind<HN_KIND_FP8>(a, g128, epilogue, out_dtype, st);

@@ -22,7 +22,9 @@
 // Group modes.  group == K (per-token activations x per-channel weights): one integer (int8) or fp32 (fp8)
 // accumulator across the whole K, dequantized once in the epilogue.  group == 128 (the reference's g128
 // layout): the stages of one 128-byte group produce its partial, which is folded into an fp32 accumulator
-// with acc = fma(float(part) * sa[m, g], sw[n, g], acc); the group's scales ride along in LDS.
+// with acc = fma(float(part) * sa[m, g], sw[n, g], acc); the group's scales ride along in LDS.  With the
+// fp8 128 x 128 block weight scales (one scale row per 128 channels) the fold is
+// acc = fma(float(part), sa[m, g] * sw[block, g], acc): one VALU op per output and group.
 //
 // Workgroup order.  Consecutive workgroup ids are dealt round-robin to the 8 XCDs; the id is remapped so
 // each XCD owns a contiguous range of tiles, which are then visited in column groups of 8 token tiles so
@@ -42,6 +44,7 @@ struct GemmArgs {
   int64_t ldw;
   const float* sw;
   int64_t ldsw;
+  int sw_rows;  // output channels per weight-scale row: 1, or 128 (fp8 128 x 128 block scales)
   const void* bias;
   int bias_dtype;
   int64_t M, N, K;
@@ -174,7 +177,7 @@ __device__ __forceinline__ uint32_t cvt2_out(float a, float b) {
 // at any time are consecutive (8 token tiles x 4 channel tiles share their panels in that XCD's L2).
 // The first stage of the next tile is issued before the current tile's epilogue, so its load latency
 // hides behind the epilogue and the epilogue's stores drain while it lands.
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS>
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK>
 __global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WN * WM / 4, WN * WM / 4)))
 void block_gemm_kernel(const GemmArgs a) {
   using MF = Mfma<KIND>;
@@ -198,6 +201,9 @@ void block_gemm_kernel(const GemmArgs a) {
   static_assert(SLICES >= 2 && SLICES % 2 == 0, "fragment sets alternate per slice, starting each stage at set 0");
   static_assert(kGroupK % BK == 0, "stage size");
   static_assert(EPI != HN_EPI_GELU_QUANT || TN * 32 == 128, "gelu_quant needs a 128-channel wave tile");
+  // WBLK: one weight-scale row per 128 output channels (the fp8 128 x 128 block layout); a wave's TN * 32
+  // channels then lie in one block, so the group fold multiplies by one scale product per token
+  static_assert(!WBLK || (G128 && (TN * 32) % 128 == 0 && BN % 128 == 0), "block weight scales");
   // Epilogue staging of 2-byte outputs, one block of 32 tokens at a time: each wave transposes its
   // 32 x BNW sub-tile through LDS (token-major rows padded by 16 bytes) so the stores are full 16-byte
   // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage);
@@ -266,8 +272,13 @@ void block_gemm_kernel(const GemmArgs a) {
     for (int u = 0; u < SC_PER_WAVE; u++) {
       const int q = wave + NW * u;
       if (q < BN / 64) {
-        scbase[u] = a.sw + n0 * a.ldsw;
-        scoff[u] = (uint32_t)min(q * 64 + lane, nlim) * (uint32_t)a.ldsw;
+        if constexpr (WBLK) {  // the scale row of the channel's 128-block (n0 is a multiple of 128)
+          scbase[u] = a.sw + (n0 / 128) * a.ldsw;
+          scoff[u] = (uint32_t)(min(q * 64 + lane, nlim) / 128) * (uint32_t)a.ldsw;
+        } else {
+          scbase[u] = a.sw + n0 * a.ldsw;
+          scoff[u] = (uint32_t)min(q * 64 + lane, nlim) * (uint32_t)a.ldsw;
+        }
       } else if (q < SC_SLOTS) {
         scbase[u] = a.sa + m0 * a.ldsa;
         scoff[u] = (uint32_t)min((q - BN / 64) * 64 + lane, mlim) * (uint32_t)a.ldsa;
@@ -364,19 +375,27 @@ void block_gemm_kernel(const GemmArgs a) {
       if constexpr (G128) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
           const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
+          const float swb = WBLK ? sc[wn * TN * 32] : 0.0f;  // the wave's one weight scale (block layout)
 #pragma unroll
           for (int j = 0; j < TM; j++) {
             const float sam = sc[BN + wrow_m + j * 32];
+            const float ss = sam * swb;
 #pragma unroll
             for (int i = 0; i < TN; i++) {
 #pragma unroll
               for (int rr = 0; rr < 4; rr++) {
-                const float4 swv =
-                    *reinterpret_cast<const float4*>(sc + wn * TN * 32 + i * 32 + rr * 8 + (lane >> 5) * 4);
-                facc[i][j][rr * 4 + 0] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 0]) * sam, swv.x, facc[i][j][rr * 4 + 0]);
-                facc[i][j][rr * 4 + 1] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 1]) * sam, swv.y, facc[i][j][rr * 4 + 1]);
-                facc[i][j][rr * 4 + 2] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 2]) * sam, swv.z, facc[i][j][rr * 4 + 2]);
-                facc[i][j][rr * 4 + 3] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 3]) * sam, swv.w, facc[i][j][rr * 4 + 3]);
+                if constexpr (WBLK) {
+#pragma unroll
+                  for (int qq = 0; qq < 4; qq++)
+                    facc[i][j][rr * 4 + qq] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + qq]), ss, facc[i][j][rr * 4 + qq]);
+                } else {
+                  const float4 swv =
+                      *reinterpret_cast<const float4*>(sc + wn * TN * 32 + i * 32 + rr * 8 + (lane >> 5) * 4);
+                  facc[i][j][rr * 4 + 0] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 0]) * sam, swv.x, facc[i][j][rr * 4 + 0]);
+                  facc[i][j][rr * 4 + 1] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 1]) * sam, swv.y, facc[i][j][rr * 4 + 1]);
+                  facc[i][j][rr * 4 + 2] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 2]) * sam, swv.z, facc[i][j][rr * 4 + 2]);
+                  facc[i][j][rr * 4 + 3] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 3]) * sam, swv.w, facc[i][j][rr * 4 + 3]);
+                }
               }
             }
           }

@@ -30,7 +30,7 @@ SIGNATURES = {
     "hn_version": ([], _i),
     "hn_last_error": ([], ctypes.c_char_p),
     "hn_quantize_act": ([_p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _i64, _p, _i64, _p], _i),
-    "hn_block_gemm": ([_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _i,
+    "hn_block_gemm": ([_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _i,
                        _i64, _p, _i64, _p], _i),
     "hn_adaln": ([_p, _p, _p, _i, _i64, _i64, _i64, _f, _i, _p, _p], _i),
     "hn_adaln_quant": ([_p, _p, _p, _i, _i64, _i64, _i64, _f, _i, _i, _i64, _p, _p, _p], _i),

@@ -63,7 +63,8 @@ def _scales(s, rows, groups):
 def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8", epilogue=None):
     """Block-scaled GEMM on quantized activations (hy_nomas/kernels.py:152-170).  With epilogue
     "gelu_quant" returns (int8 [M, N], scales [M, N / 128]) ready for the next int8 linear; otherwise
-    [M, N] in `out_dtype`."""
+    [M, N] in `out_dtype`.  Weight scales are [N, K/128] or [N, 1] (one row per output channel), or
+    [ceil(N/128), K/128]: one row per 128 output channels (the fp8 128 x 128 block layout)."""
     _lib.require_device(qa, sa, qw, sw, bias)
     m, k = qa.shape
     n = qw.shape[0]
@@ -76,19 +77,23 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
         qs = None
     if m == 0:
         return (out, qs) if mode == 2 else out
+    # weight scales with one row per channel, or one row per 128 channels (block layout, g128 fold only)
+    sw_rows = 1 if sw.shape[0] == n else GROUP
+    if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
+        raise RuntimeError(f"weight scales with {sw.shape[0]} rows for {n} output channels")
     # one scale per token and per channel -> whole-K accumulation; otherwise the g128 fold
-    if sa.shape[1] == 1 and sw.shape[1] == 1:
+    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1:
         group, groups = k, 1
     else:
         group, groups = GROUP, k // GROUP
     sa = _scales(sa, m, groups)
-    sw = _scales(sw, n, groups)
+    sw = _scales(sw, sw.shape[0], groups)
     qa = _rows(qa)
     qw = _rows(qw)
     if bias is not None and not bias.is_contiguous():
         bias = bias.contiguous()
     _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
-              sw.data_ptr(), sw.stride(0), _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
+              sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
               m, n, k, group, _lib.KIND[kind], mode, out.data_ptr(), _lib.dtype_code(out) if mode != 2 else 0,
               out.stride(0), _lib.ptr(qs), qs.stride(0) if qs is not None else 0, _lib.stream(qa))
     return (out, qs) if mode == 2 else out
@@ -104,7 +109,7 @@ def block_gemm_acc32(qa, qw):
         return out
     qa = _rows(qa)
     qw = _rows(qw)
-    _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), None, 0, qw.data_ptr(), qw.stride(0), None, 0, None, 0,
+    _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), None, 0, qw.data_ptr(), qw.stride(0), None, 0, 1, None, 0,
               m, n, k, k, _lib.KIND["int8"], _lib.EPI_ACC32, out.data_ptr(), 0, out.stride(0), None, 0,
               _lib.stream(qa))
     return out
@@ -133,13 +138,16 @@ def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away", g
 def block_linear(x, qw, sw, bias=None, kind="int8"):
     """F.linear with block-scaled 8-bit weights: x [..., K] -> [..., N] in x's dtype
     (hy_nomas/kernels.py:210-222).  Weight scales [N, K/128] select per-token-and-group activation
-    quantization; per-channel scales [N, 1] select per-token quantization."""
+    quantization; per-channel scales [N, 1] select per-token quantization; block scales
+    [ceil(N/128), K/128] (one row per 128 output channels) are taken as they are."""
     shape = x.shape
     x2 = x.reshape(-1, shape[-1])
     if not x2.is_contiguous():
         x2 = x2.contiguous()
     if shape[-1] % GROUP or x2.shape[0] == 0:
         from .ops import dequantize_g128
+        if sw.shape[0] != qw.shape[0]:
+            sw = sw.repeat_interleave(GROUP, dim=0)[: qw.shape[0]]
         return torch.nn.functional.linear(x, dequantize_g128(qw, sw, x.dtype), bias)
     group = None if sw.shape[1] == 1 else GROUP
     with torch.cuda.device(x.device):

@@ -29,10 +29,11 @@ def dequantize_fp8_block(qdata, scale, dtype=torch.bfloat16):
 
 
 def fp8_block_linear(x, qdata, scale, bias=None):
-    """F.linear with fp8 block weights on the fp8 matrix cores: the block scales are expanded to one per
-    row and 128-group, activations are quantized to e4m3 per token and 128 channels
-    (hy_nomas/pixelumm.py:147-155)."""
-    return kernels.block_linear(x, qdata, scale.repeat_interleave(128, dim=0), bias, kind="fp8")
+    """F.linear with fp8 block weights on the fp8 matrix cores, activations quantized to e4m3 per token
+    and 128 channels (hy_nomas/pixelumm.py:147-155).  The reference expands the block scales to one row
+    per output channel; here the GEMM reads the [N/128, K/128] block scales directly, one scale product
+    per token and 128-block in the group fold."""
+    return kernels.block_linear(x, qdata, scale, bias, kind="fp8")
 
 
 class DecoderOps:

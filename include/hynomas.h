@@ -64,8 +64,13 @@ int hn_quantize_act(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * part_g the exact int32 (int8) or fp32 (fp8) dot product of group g; the sum runs in group order as
  * acc = fma(part * sa, sw, acc).
  *   qa [M, K] codes (row stride lda), qw [N, K] codes (row stride ldw, K-major: the NT layout),
- *   sa [M, K / group] (row stride ldsa), sw [N, K / group] (row stride ldsw), fp32;
+ *   sa [M, K / group] (row stride ldsa), sw [N / sw_rows, K / group] (row stride ldsw), fp32;
  *   bias [N] of bias_dtype or NULL.
+ * sw_rows = 1: one weight-scale row per output channel (the reference's layout).  sw_rows = 128 (group
+ * 128 only): one row per 128 output channels, sw [ceil(N / 128), K / 128] -- the 128 x 128 block scales
+ * of the FP8 block-128 weight layout (hy_nomas/pixelumm.py:60-63, 77-82) without the repeat_interleave
+ * its fp8 linear applies before block_linear (pixelumm.py:147-152); the fold is then
+ * acc = fma(part, sa * sw, acc).
  * group = 128 (the reference's g128 layout) or K (per-token activations x per-channel weights).
  * epilogue NONE: out [M, N] of out_dtype.  GELU: out = bf16(gelu_tanh(bf16(acc))) (kernels.py:125-128).
  * GELU_QUANT: out int8 [M, N] codes of the GELU output, quantized per row and 128 columns, with scales
@@ -74,7 +79,7 @@ int hn_quantize_act(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * K % 128 == 0; M, N >= 1.
  */
 int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
-                  const float* sw, int64_t ldsw, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K,
+                  const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K,
                   int64_t group, int kind, int epilogue, void* out, int out_dtype, int64_t ldo, float* qs,
                   int64_t ldqs, void* stream);
 

@@ -45,13 +45,19 @@ def test_argument_validation_without_a_gpu():
     assert l.hn_version() >= 100
     rc = l.hn_quantize_act(None, 0, 100, 4, 100, 128, 0, 0, None, 100, None, 1, None)   # K % 128 != 0
     assert rc == 1 and b"multiple of 128" in l.hn_last_error()
-    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, None, 0, 4, 8, 256, 64, 0, 0, None, 0, 8, None, 0,
-                         None)   # group 64
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 4, 8, 256, 64, 0, 0, None, 0, 8, None,
+                         0, None)   # group 64
     assert rc == 1 and b"group" in l.hn_last_error()
     rc = l.hn_adaln_quant(None, None, None, 0, 1, 4, 200, 1e-6, 0, 0, 128, None, None, None)   # D % 128 != 0
     assert rc == 1 and b"multiple of 128" in l.hn_last_error()
     rc = l.hn_qk_norm_rope(None, 96, None, None, None, 1, 1, 1, 96, 1e-6, None, None)   # head dim 96
     assert rc == 1
-    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, None, 0, 4, 8, 256, 128, 0, 7, None, 0, 8, None,
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 4, 8, 256, 128, 0, 7, None, 0, 8, None,
                          0, None)   # bad epilogue
     assert rc == 1
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 64, None, 0, 4, 8, 256, 128, 1, 0, None, 0, 8, None,
+                         0, None)   # weight-scale rows of 64 channels
+    assert rc == 1 and b"sw_rows" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 256, None, 1, None, 256, None, 1, 128, None, 0, 4, 8, 256, 256, 1, 0, None, 0, 8, None,
+                         0, None)   # block weight scales need group 128
+    assert rc == 1 and b"sw_rows" in l.hn_last_error()

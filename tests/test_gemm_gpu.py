@@ -178,3 +178,58 @@ def test_fp8_gemm(dev, m, n, k, group):
     exact = fp64_dequant_product(qa, sa, w_codes, sw_full.numpy(), bias, kind="fp8")
     assert max_abs_rel(out, exact) < 1e-2
     assert max_abs_rel(out, ref) < 4e-3
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+@pytest.mark.parametrize("m,n,k", [(300, 384, 1024), (1024, 1536, 3072), (77, 200, 256), (64, 256, 128)])
+def test_block_weight_scales(dev, kind, m, n, k):
+    """Weight scales with one row per 128 output channels ([ceil(N/128), K/128], the fp8 128 x 128 block
+    layout) against the same GEMM on the scales expanded to one row per channel: the fold multiplies by
+    the product sa * sw instead of by sa, then sw, so the two agree to fp32 rounding, and both match the
+    fp64 product of the dequantized operands."""
+    from hy_nomas import kernels
+
+    print(f"block weight scales {kind} m={m} n={n} k={k}", flush=True)
+    g = seeded(m * 7 + n + k)
+    x = outlier_input(m, k, seed=m + 1)
+    nb = (n + 127) // 128
+    sblk = (torch.rand(nb, k // 128, generator=g) * 4e-3 + 1e-3).float()
+    if kind == "fp8":
+        codes = (torch.randn(n, k, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+        w_codes = codes.view(torch.uint8).numpy()
+    else:
+        codes = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+        w_codes = codes.numpy()
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    sw_full = sblk.repeat_interleave(128, 0)[:n].contiguous()
+    qa, sa = oracle.quantize(x, 128, kind)
+    qa_t = torch.from_numpy(qa)
+    if kind == "fp8":
+        qa_t = qa_t.view(torch.float8_e4m3fn)
+    args = (qa_t.to(dev), torch.from_numpy(sa).to(dev), codes.to(dev))
+    # fp32 outputs, so that the fold's rounding is not hidden behind (or magnified by) a bf16 rounding
+    got = kernels.block_gemm(*args, sblk.to(dev), bias.to(dev), torch.float32, kind=kind).cpu().numpy()
+    full = kernels.block_gemm(*args, sw_full.to(dev), bias.to(dev), torch.float32, kind=kind).cpu().numpy()
+    exact = fp64_dequant_product(qa, sa, w_codes, sw_full.numpy(), bias, kind=kind)
+    assert max_abs_rel(got, exact) < 1e-2
+    assert max_abs_rel(got, full) < 4e-3
+    if kind == "int8":   # exact int32 partials: only the fold's fp32 rounding differs
+        assert max_abs_rel(got, full) < 1e-4
+
+
+def test_fp8_block_linear(dev):
+    """pixelumm.fp8_block_linear (block scales read directly) against F.linear on the dequantized fp8
+    weights in fp32 (hy_nomas/pixelumm.py:147-155)."""
+    from hy_nomas import pixelumm
+
+    print("fp8 block linear", flush=True)
+    g = seeded(4242)
+    x = (torch.randn(3, 170, 1024, generator=g) * 0.5).to(torch.bfloat16)
+    w = torch.randn(768, 1024, generator=g) * 0.02
+    bias = (torch.randn(768, generator=g) * 0.02).to(torch.bfloat16)
+    qw, sblk = pixelumm.quantize_fp8_block(w)
+    got = pixelumm.fp8_block_linear(x.to(dev), qw.to(dev), sblk.to(dev), bias.to(dev)).cpu().float()
+    ref = torch.nn.functional.linear(x.float(), pixelumm.dequantize_fp8_block(qw, sblk, torch.float32),
+                                     bias.float())
+    assert got.shape == (3, 170, 768)
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 3e-2
