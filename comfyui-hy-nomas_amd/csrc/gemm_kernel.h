@@ -206,14 +206,17 @@ void block_gemm_kernel(const GemmArgs a) {
   static_assert(!WBLK || (G128 && (TN * 32) % 128 == 0 && BN % 128 == 0), "block weight scales");
   // Epilogue staging of 2-byte outputs, one block of 32 tokens at a time: each wave transposes its
   // 32 x BNW sub-tile through LDS (token-major rows padded by 16 bytes) so the stores are full 16-byte
-  // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage);
-  // the per-channel scales and bias of the tile follow it.
+  // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage).
+  // The tile's epilogue operands (per-channel scales and bias, per-token scales) are written at the tile
+  // top, while stage buffer 1 fills, so they lie past both the staging area and the stage ring.
   constexpr bool STAGED = OUT_DT != HN_DTYPE_F32 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU);
   constexpr int OPITCH = TN * 32 * 2 + 16;
   constexpr int STG_OFF = SCR + STAGE;
-  constexpr int EP_OFF = STG_OFF + (STAGED ? NW * 32 * OPITCH : 0);
   constexpr int RING_END = SCR + NS * STAGE;
-  constexpr int SMEM = EP_OFF + 2 * BN * 4 > RING_END ? EP_OFF + 2 * BN * 4 : RING_END;
+  constexpr int STG_END = STG_OFF + (STAGED ? NW * 32 * OPITCH : 0);
+  constexpr int EP_OFF = STG_END > RING_END ? STG_END : RING_END;
+  constexpr int EP_BYTES = EPI == HN_EPI_ACC32 ? 0 : (2 * BN + BM) * 4;  // sw | bias | sa of the tile
+  constexpr int SMEM = EP_OFF + EP_BYTES > RING_END ? EP_OFF + EP_BYTES : RING_END;
   __shared__ __align__(16) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -343,10 +346,46 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; r++) facc[i][j][r] = 0.0f;
     }
-    // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging reads
-    // of the previous epilogue are done, so buffer 1 is free
+    // The tile's epilogue operands (per-channel weight scale and bias, per-token activation scale) are
+    // fetched here, so their latency overlaps the wait for stage 0, and parked in LDS for the epilogue.
+    // Rows and channels past the edge take the last valid one; an absent bias reads as -0.0, which
+    // leaves every sum (signed zeros included) unchanged.
+    constexpr int EP_PER = EPI == HN_EPI_ACC32 ? 0 : (BN + NW * 64 - 1) / (NW * 64);
+    constexpr int EPM_PER = EPI == HN_EPI_ACC32 || G128 ? 0 : (BM + NW * 64 - 1) / (NW * 64);
+    float ep_sw[EP_PER > 0 ? EP_PER : 1], ep_b[EP_PER > 0 ? EP_PER : 1], ep_sa[EPM_PER > 0 ? EPM_PER : 1];
+    {
+      const int64_t nleft0 = a.N - n0, mleft0 = a.M - m0;
+      const int nlast = nleft0 < BN ? (int)nleft0 - 1 : BN - 1, mlast = mleft0 < BM ? (int)mleft0 - 1 : BM - 1;
+#pragma unroll
+      for (int u = 0; u < EP_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        const int64_t n = n0 + (tt < nlast ? tt : nlast);
+        ep_sw[u] = G128 ? 0.0f : a.sw[n * a.ldsw];
+        ep_b[u] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : -0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < EPM_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        ep_sa[u] = a.sa[(m0 + (tt < mlast ? tt : mlast)) * a.ldsa];
+      }
+    }
+    // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging and
+    // operand reads of the previous epilogue are done, so buffer 1 and the operand area are free
     wait_vmcnt<0>();
     barrier();
+    if constexpr (EPI != HN_EPI_ACC32) {
+      float* ep = reinterpret_cast<float*>(smem + EP_OFF);
+#pragma unroll
+      for (int u = 0; u < EP_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        if (tt < BN) { ep[tt] = ep_sw[u]; ep[BN + tt] = ep_b[u]; }
+      }
+#pragma unroll
+      for (int u = 0; u < EPM_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        if (tt < BM) ep[2 * BN + tt] = ep_sa[u];
+      }
+    }
     if (1 < nk) issue_stage(1, 1);
     read_frags(0, smem + SCR, 0);
 
@@ -446,22 +485,13 @@ void block_gemm_kernel(const GemmArgs a) {
         }
       }
     } else {
-      // Per-channel scale (per-token mode) and bias of the tile's BN channels, staged in LDS.
-      float* ep = reinterpret_cast<float*>(smem + EP_OFF);
-      for (int tt = tid; tt < BN; tt += NW * 64) {
-        const int64_t n = en0 + min(tt, nrem - 1);
-        ep[tt] = G128 ? 0.0f : a.sw[n * a.ldsw];
-        ep[BN + tt] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : 0.0f;
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the ds_writes above have landed
-      barrier();
-      const bool has_bias = a.bias != nullptr;
-      const float* sabase = a.sa + em0 * a.ldsa;
+      // per-channel scale and bias, and per-token scale, of this tile (written at the tile top)
+      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF);
 #pragma unroll
       for (int j = 0; j < TM; j++) {
         const int ml = erow_m + j * 32;
         const bool m_ok = ml < mrem;
-        const float sam = G128 ? 0.0f : sabase[(uint32_t)(min(ml, mrem - 1) * (int)a.ldsa)];
+        const float sam = G128 ? 0.0f : ep[2 * BN + ml];
         // dequantize + bias (+ GELU) in place; the results overwrite the accumulator registers as fp32 bits
 #pragma unroll
         for (int i = 0; i < TN; i++) {
@@ -477,7 +507,7 @@ void block_gemm_kernel(const GemmArgs a) {
               float v;
               if constexpr (G128) v = facc[i][j][r];
               else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
-              if (has_bias) v = v + bq[q];
+              v = v + bq[q];
               if constexpr (EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT) v = rbf16(gelu_tanh(rbf16(v)));
               MF::put(acc[i][j], r, v);
             }
