@@ -31,6 +31,8 @@
 // that concurrently running tiles share weight and activation panels in that XCD's L2.
 #pragma once
 
+#include <type_traits>
+
 #include "hn_common.h"
 
 namespace hn {
@@ -177,7 +179,8 @@ __device__ __forceinline__ uint32_t cvt2_out(float a, float b) {
 // at any time are consecutive (8 token tiles x 4 channel tiles share their panels in that XCD's L2).
 // The first stage of the next tile is issued before the current tile's epilogue, so its load latency
 // hides behind the epilogue and the epilogue's stores drain while it lands.
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK>
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK,
+          bool AV = false>
 __global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WN * WM / 4, WN * WM / 4)))
 void block_gemm_kernel(const GemmArgs a) {
   using MF = Mfma<KIND>;
@@ -291,17 +294,36 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     }
   };
+  // AV: the activation tile goes through registers (global loads into astg, then LDS writes once they
+  // land) while the weight tile streams straight into LDS; the two paths run side by side.
+  v4i astg[AV ? B_KB : 1];
   auto issue_stage = [&](int kt, int buf) {
     char* base = smem + SCR + buf * STAGE;
     const uint8_t* wk = wbase + (int64_t)kt * BK;
     const uint8_t* ak = abase + (int64_t)kt * BK;
+    if constexpr (AV) {
+#pragma unroll
+      for (int u = 0; u < B_KB; u++) astg[u] = *reinterpret_cast<const v4i*>(ak + aoff[u]);
+    }
 #pragma unroll
     for (int u = 0; u < A_KB; u++) g2lds16(wk + woff[u], base + (wave + NW * u) * 1024);
+    if constexpr (!AV) {
 #pragma unroll
-    for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
+      for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
+    }
 #pragma unroll
     for (int u = 0; u < SC_PER_WAVE; u++)
       g2lds4(scbase[u] + kt / STAGES_PER_GROUP + scoff[u], smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
+  };
+
+  // AV: the activation tile of a landed stage, from registers into buffer `buf` (same LDS layout as the
+  // direct loads: lane i's 16 bytes at block base + 16 i)
+  auto commit_stage = [&](int buf) {
+    if constexpr (AV) {
+      char* base = smem + SCR + buf * STAGE + A_BYTES;
+#pragma unroll
+      for (int u = 0; u < B_KB; u++) *reinterpret_cast<v4i*>(base + (wave + NW * u) * 1024 + lane * 16) = astg[u];
+    }
   };
 
   const int nk = (int)(a.K / BK);
@@ -372,6 +394,8 @@ void block_gemm_kernel(const GemmArgs a) {
     // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging and
     // operand reads of the previous epilogue are done, so buffer 1 and the operand area are free
     wait_vmcnt<0>();
+    commit_stage(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     barrier();
     if constexpr (EPI != HN_EPI_ACC32) {
       float* ep = reinterpret_cast<float*>(smem + EP_OFF);
@@ -389,27 +413,62 @@ void block_gemm_kernel(const GemmArgs a) {
     if (1 < nk) issue_stage(1, 1);
     read_frags(0, smem + SCR, 0);
 
-    int buf = 0;
-    for (int kt = 0; kt < nk; kt++) {
+    // products of weight fragments [i0, i1) with every activation fragment of register set `set`
+    auto mfma_rows = [&](int set, int i0, int i1) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = i0; i < i1; i++)
+#pragma unroll
+        for (int j = 0; j < TM; j++) acc[i][j] = MF::run(fa[set][i], fb[set][j], acc[i][j]);
+    };
+    // One K stage (kt, in buffer `buf`).  The schedule is pinned with scheduling barriers (address
+    // arithmetic may still move): each slice issues the next slice's fragment reads right after its
+    // first products, so they land while the matrix core works.  The last slice holds the stage
+    // barrier; after it the next stage's first fragments are read and the direct loads of stage kt + 2
+    // are interleaved with the slice's remaining products, so the matrix core is fed while the loads
+    // queue.  MODE 0: barrier and loads; 1: barrier, no loads (stage kt + 2 does not exist); 2: the
+    // tile's last stage (neither).
+    constexpr int PRE = 1;                                   // weight rows multiplied before the barrier
+    constexpr int POST_MFMA = (TN - PRE) * TM;
+    constexpr int VM_LOADS = A_KB + (AV ? 0 : B_KB) + SC_PER_WAVE;
+    constexpr int VM_PER = (VM_LOADS + POST_MFMA - 1) / POST_MFMA;
+    auto stage_body = [&](int kt, int buf, auto mode_c) __attribute__((always_inline)) {
+      constexpr int MODE = decltype(mode_c)::value;
       const char* stage = smem + SCR + buf * STAGE;
 #pragma unroll
       for (int s = 0; s < SLICES; s++) {
         const int cur = s & 1;
         if (s + 1 < SLICES) {
+          mfma_rows(cur, 0, 1);
+          __builtin_amdgcn_sched_barrier(0x6);
           read_frags(cur ^ 1, stage, s + 1);
-        } else if (kt + 1 < nk) {
+          __builtin_amdgcn_sched_barrier(0x6);
+          mfma_rows(cur, 1, TN);
+          __builtin_amdgcn_sched_barrier(0x6);
+        } else if constexpr (MODE == 2) {
+          mfma_rows(cur, 0, TN);
+        } else {
+          mfma_rows(cur, 0, PRE);
+          // (the waits and the barrier are scalar instructions: nothing may cross them)
+          __builtin_amdgcn_sched_barrier(0);
           // stage kt + 1 (the only loads in flight) has landed for this wave and its reads of stage kt
-          // are complete; the barrier publishes both facts, then stage kt + 2 may refill buffer `buf`
+          // are complete; the barrier publishes both facts, then stage kt + 2 may refill `buf`
           wait_vmcnt<0>();
+          commit_stage(buf ^ 1);
           __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
           barrier();
-          if (kt + 2 < nk) issue_stage(kt + 2, buf);
+          __builtin_amdgcn_sched_barrier(0);
           read_frags(cur ^ 1, smem + SCR + (buf ^ 1) * STAGE, 0);
+          if constexpr (MODE == 0) issue_stage(kt + 2, buf);
+          mfma_rows(cur, PRE, TN);
+          // reads first, then products and loads alternating
+          __builtin_amdgcn_sched_group_barrier(0x100, TN + TM, 0);
+#pragma unroll
+          for (int r = 0; r < POST_MFMA; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if constexpr (MODE == 0) __builtin_amdgcn_sched_group_barrier(0x020, VM_PER, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0x6);
         }
-#pragma unroll
-        for (int i = 0; i < TN; i++)
-#pragma unroll
-          for (int j = 0; j < TM; j++) acc[i][j] = MF::run(fa[cur][i], fb[cur][j], acc[i][j]);
       }
       if constexpr (G128) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
@@ -446,8 +505,14 @@ void block_gemm_kernel(const GemmArgs a) {
               for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
         }
       }
-      buf ^= 1;
+    };
+    int kt = 0;
+    for (; kt + 2 < nk; kt++) stage_body(kt, kt & 1, std::integral_constant<int, 0>());
+    if (kt + 1 < nk) {
+      stage_body(kt, kt & 1, std::integral_constant<int, 1>());
+      kt++;
     }
+    stage_body(kt, kt & 1, std::integral_constant<int, 2>());
     // every wave is done reading the stage buffers (and the scale ring) of this tile
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     barrier();
