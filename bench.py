@@ -267,6 +267,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--block-only", action="store_true", help="only the DiT block forward (both layouts)")
+    ap.add_argument("--only", choices=["fp8", "g128", "elementwise"],
+                    help="only one of the extra measurements (for per-kernel profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 512 MiB five times (HBM counter calibration)")
     args = ap.parse_args()
@@ -289,6 +291,19 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(), "launches": 5}))
         return
 
+    if args.only == "fp8":
+        ms_f, per_f, ops = gemm_stack(dev, gen, args.steps, args.warmup, kind="fp8")
+        print(json.dumps({"fp8_block_gemm_stack_ms": round(ms_f, 4), "per_gemm_ms": [round(t, 4) for t in per_f],
+                          "TFLOPS": round(ops / (ms_f * 1e-3) / 1e12, 1)}))
+        return
+    if args.only == "g128":
+        ms_g, per_g, ops = gemm_stack(dev, gen, args.steps, args.warmup, group_mode="g128")
+        print(json.dumps({"int8_g128_stack_ms": round(ms_g, 4), "per_gemm_ms": [round(t, 4) for t in per_g],
+                          "TOPS": round(ops / (ms_g * 1e-3) / 1e12, 1)}))
+        return
+    if args.only == "elementwise":
+        print(json.dumps(elementwise(dev, gen, max(10, args.steps), 3)))
+        return
     if args.block_only:
         with torch.no_grad():
             print(json.dumps({("per_token" if pt else "g128"): dit_block(dev, gen, 3, 1, pt) for pt in (True, False)}))
