@@ -173,11 +173,14 @@ def elementwise(dev, gen, steps, warmup):
     out = {}
     for name, (fn, bpe) in cases.items():
         fns = [lambda s=s, fn=fn: fn(s) for s in sets]
-        _, per = time_launches(fns, steps, warmup)
-        us = 1e3 * sum(per) / len(per)
+        total_ms, per = time_launches(fns, steps, warmup)
+        # us: back-to-back launches on one stream (the kernel's throughput, launch gaps included);
+        # us_event: an event pair around each launch (adds the event overhead)
+        us = 1e3 * total_ms / len(fns)
         nbytes = bpe * n_el
         out[name] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
-                     "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3), "bytes": int(nbytes)}
+                     "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3), "bytes": int(nbytes),
+                     "us_event": round(1e3 * sum(per) / len(per), 2)}
     del sets
     torch.cuda.empty_cache()
     return out
