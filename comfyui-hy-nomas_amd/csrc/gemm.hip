@@ -40,7 +40,10 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
 // 128-byte K stages in two LDS buffers.
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
-  if (g128 && a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2, true>(a, st);
+  // fp8 with block weight scales rescales its running sum in place (no second accumulator set), so it
+  // fits the 256 x 256 tile
+  if (g128 && a.sw_rows == 128)
+    return launch_cfg<KIND, EPI, true, 2, 4, 4, KIND == HN_KIND_FP8 ? 2 : 1, OUT_DT, 128, 2, true>(a, st);
   if (g128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
   return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
 }

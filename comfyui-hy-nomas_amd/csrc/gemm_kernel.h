@@ -207,6 +207,11 @@ void block_gemm_kernel(const GemmArgs a) {
   // WBLK: one weight-scale row per 128 output channels (the fp8 128 x 128 block layout); a wave's TN * 32
   // channels then lie in one block, so the group fold multiplies by one scale product per token
   static_assert(!WBLK || (G128 && (TN * 32) % 128 == 0 && BN % 128 == 0), "block weight scales");
+  // RESCALE (fp8 with block weight scales): no separate fp32 running sum.  The matrix core accumulates
+  // every group straight into acc, kept in units of the current group's scale product: at each group
+  // boundary acc *= ss_g / ss_{g+1} (one VALU op per output), and the epilogue multiplies by the last
+  // group's ss.  ss_g = sa[m, g] * sw[block, g] is positive (both quantizers floor their scales).
+  constexpr bool RESCALE = G128 && WBLK && KIND == HN_KIND_FP8;
   // Epilogue staging of 2-byte outputs, one block of 32 tokens at a time: each wave transposes its
   // 32 x BNW sub-tile through LDS (token-major rows padded by 16 bytes) so the stores are full 16-byte
   // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage).
@@ -353,14 +358,15 @@ void block_gemm_kernel(const GemmArgs a) {
     asm volatile("" : "+v"(tl));
     // ---- main loop of tile (m0, n0); its stage 0 is in flight into buffer 0
     Acc acc[TN][TM];                            // MFMA accumulators (whole K, or one group in g128 mode)
-    v16f facc[G128 ? TN : 1][G128 ? TM : 1];    // g128: fp32 running sum over groups
+    v16f facc[G128 && !RESCALE ? TN : 1][G128 && !RESCALE ? TM : 1];  // g128: fp32 running sum over groups
+    float ss_last[TM];                          // RESCALE: the last group's scale product per token
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
       for (int j = 0; j < TM; j++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
-    if constexpr (G128) {
+    if constexpr (G128 && !RESCALE) {
 #pragma unroll
       for (int i = 0; i < TN; i++)
 #pragma unroll
@@ -470,7 +476,27 @@ void block_gemm_kernel(const GemmArgs a) {
           __builtin_amdgcn_sched_barrier(0x6);
         }
       }
-      if constexpr (G128) {
+      if constexpr (RESCALE) {
+        static_assert(STAGES_PER_GROUP == 1, "one group per stage");
+        const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
+        const float swb = sc[wn * TN * 32];  // the wave's one weight scale
+        if constexpr (MODE == 2) {
+#pragma unroll
+          for (int j = 0; j < TM; j++) ss_last[j] = sc[BN + wrow_m + j * 32] * swb;
+        } else {
+          // the next group's scales landed with stage kt + 1 (published by this stage's barrier)
+          const float* sn = reinterpret_cast<const float*>(smem + ((kt + 1) % (NS + 1)) * SC_BYTES);
+          const float swn = sn[wn * TN * 32];
+#pragma unroll
+          for (int j = 0; j < TM; j++) {
+            const float rho = (sc[BN + wrow_m + j * 32] * swb) / (sn[BN + wrow_m + j * 32] * swn);
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int r = 0; r < 16; r++) acc[i][j][r] *= rho;
+          }
+        }
+      } else if constexpr (G128) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
           const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
           const float swb = WBLK ? sc[wn * TN * 32] : 0.0f;  // the wave's one weight scale (block layout)
@@ -570,7 +596,8 @@ void block_gemm_kernel(const GemmArgs a) {
             for (int q = 0; q < 4; q++) {
               const int r = rr * 4 + q;
               float v;
-              if constexpr (G128) v = facc[i][j][r];
+              if constexpr (RESCALE) v = MF::get(acc[i][j], r) * ss_last[j];
+              else if constexpr (G128) v = facc[i][j][r];
               else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
               v = v + bq[q];
               if constexpr (EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT) v = rbf16(gelu_tanh(rbf16(v)));
