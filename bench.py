@@ -148,6 +148,28 @@ def linear_stack_with_quant(dev, gen, steps, warmup):
     return ms
 
 
+def kv_history(dev, gen, steps, warmup):
+    """int8 K/V history of the config-4 block: K [57344, 24, 128] bf16, quantized per (token, head) and
+    dequantized back to bf16, two rotating slabs (> the 256 MB Infinity Cache together with their codes)."""
+    from hy_nomas import kv
+
+    shape = (57344, 24, 128)
+    n_el = shape[0] * shape[1] * shape[2]
+    xs = [torch.randn(shape, generator=gen, device=dev).to(torch.bfloat16) for _ in range(2)]
+    qs = [kv.quantize_kv(x) for x in xs]
+    out = {}
+    for name, fns, nbytes in (
+            ("quantize_kv", [lambda x=x: kv.quantize_kv(x) for x in xs], n_el * (2 + 1) + n_el // 128 * 4),
+            ("dequantize_kv", [lambda q=q: kv.dequantize_kv(q[0], q[1]) for q in qs], n_el * (1 + 2) + n_el // 128 * 4)):
+        total_ms, per = time_launches(fns, steps, warmup)
+        us = 1e3 * total_ms / len(fns)
+        out[name] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                     "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3), "bytes": int(nbytes)}
+    del xs, qs
+    torch.cuda.empty_cache()
+    return out
+
+
 def elementwise(dev, gen, steps, warmup):
     """Fused elementwise kernels at x [1, 32768, 3072] bf16, three rotating input sets (576 MiB > the 256 MB
     Infinity Cache) so each launch reads cold HBM.  Returns {name: (us, GB/s, algorithmic bytes)}."""
@@ -306,6 +328,7 @@ def main():
         return
     if args.only == "elementwise":
         print(json.dumps(elementwise(dev, gen, max(10, args.steps), 3)))
+        print(json.dumps(kv_history(dev, gen, max(10, args.steps), 3)))
         return
     if args.block_only:
         with torch.no_grad():
@@ -360,6 +383,8 @@ def main():
                                    "frac_fp8_peak": round(ops / (ms_f * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 3)}
         log("bench: elementwise")
         extra["elementwise"] = elementwise(dev, gen, max(10, args.steps), 3)
+        log("bench: kv history")
+        extra["kv_history"] = kv_history(dev, gen, max(10, args.steps), 3)
         for pt in (True, False):
             name = "dit_block_M57344_" + ("per_token" if pt else "g128")
             log("bench: " + name)

@@ -29,13 +29,24 @@ __device__ __forceinline__ float round_to(float v) {
 
 // 8 fp32 values -> 8 packed 2-byte values.  FINITE: the values are known not to be NaN, so the hardware
 // bf16 conversion (equal to the torch rule on every non-NaN value) is used.
+// fp16: the fp32 values are materialized first; the compiler would otherwise fuse a producing fma with the
+// conversion into one mixed-precision fma rounding once to fp16, where the reference rounds to fp32 first.
 template <int DT, bool FINITE>
 __device__ __forceinline__ uint4 narrow8x(const float* f) {
-  if constexpr (DT == HN_DTYPE_BF16 && FINITE)
+  if constexpr (DT == HN_DTYPE_BF16 && FINITE) {
     return make_uint4(bf16x2_finite(f[0], f[1]), bf16x2_finite(f[2], f[3]), bf16x2_finite(f[4], f[5]),
                       bf16x2_finite(f[6], f[7]));
-  else
+  } else if constexpr (DT == HN_DTYPE_F16) {
+    float g[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      g[k] = f[k];
+      asm volatile("" : "+v"(g[k]));
+    }
+    return narrow8<DT>(g);
+  } else {
     return narrow8<DT>(f);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -332,6 +343,58 @@ static int launch_gated_residual(const void* x, const void* y, const void* gate,
 }
 
 // ---------------------------------------------------------------------------------------------
+// Row-scaled int8 dequantization: out[r, :] = dtype(float(q[r, :]) * s[r])      (world.py:93-94)
+// One thread per 16 codes (one 16-byte load).  A code b (as an unsigned byte after flipping its sign
+// bit) is q = b - 128, so q * s = fma(b, s, -128 s) with -128 s exact: the one rounding of the product,
+// from the single-instruction unsigned byte conversion.
+template <int DT, bool WIDE>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                                           const float* __restrict__ s, int64_t lds,
+                                                           int64_t rows, int cpr, void* __restrict__ out,
+                                                           int64_t ldo) {
+  int64_t r;
+  int c;
+  if constexpr (WIDE) {  // more than 2^32 chunks
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= rows * cpr) return;
+    r = t / cpr;
+    c = (int)(t - r * cpr);
+  } else {
+    const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= (uint32_t)(rows * cpr)) return;
+    const uint32_t r32 = t / (uint32_t)cpr;
+    r = r32;
+    c = (int)(t - r32 * (uint32_t)cpr);
+  }
+  const uint4 v = *reinterpret_cast<const uint4*>(q + r * ldq + c * 16);
+  const float sc = s[r * lds];
+  const float off = -128.0f * sc;
+  const uint32_t w[4] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u, v.w ^ 0x80808080u};
+  float f[16];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    f[4 * k + 0] = __builtin_fmaf((float)(w[k] & 0xffu), sc, off);  // v_cvt_f32_ubyte0..3
+    f[4 * k + 1] = __builtin_fmaf((float)((w[k] >> 8) & 0xffu), sc, off);
+    f[4 * k + 2] = __builtin_fmaf((float)((w[k] >> 16) & 0xffu), sc, off);
+    f[4 * k + 3] = __builtin_fmaf((float)(w[k] >> 24), sc, off);
+  }
+  if constexpr (DT == HN_DTYPE_F32) {
+    float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + r * ldo + c * 16);
+#pragma unroll
+    for (int k = 0; k < 4; k++) o[k] = make_float4(f[4 * k], f[4 * k + 1], f[4 * k + 2], f[4 * k + 3]);
+  } else {
+    uint4* o = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + c * 16);
+    if (__builtin_expect(sc == sc, 1)) {  // a NaN scale takes the software rounding (torch's NaN code)
+      o[0] = narrow8x<DT, true>(f);
+      o[1] = narrow8x<DT, true>(f + 8);
+    } else {
+      o[0] = narrow8x<DT, false>(f);
+      o[1] = narrow8x<DT, false>(f + 8);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // QK RMSNorm + interleaved RoPE                                  (fused.py:65-91)
 // W = D / 8 lanes per (token, head); 64 / W heads per wavefront.
 template <int W, bool ROPE>
@@ -491,6 +554,31 @@ extern "C" int hn_gated_residual(const void* x, const void* y, const void* gate,
   if (dtype == HN_DTYPE_F16) return launch_gated_residual<HN_DTYPE_F16>(x, y, gate, B * L, L, D, out, st);
   set_error("hn_gated_residual: unsupported dtype %d", dtype);
   return HN_ERR_UNSUPPORTED;
+}
+
+extern "C" int hn_dequantize_rows(const int8_t* q, int64_t ldq, const float* s, int64_t lds, int64_t rows,
+                                  int64_t D, void* out, int out_dtype, int64_t ldo, void* stream) {
+  HN_REQUIRE(rows >= 0 && D > 0, "hn_dequantize_rows: bad shape");
+  HN_REQUIRE(D % 16 == 0, "hn_dequantize_rows: D=%lld must be a multiple of 16", (long long)D);
+  HN_REQUIRE(ldq >= D && ldq % 16 == 0 && ldo >= D && ldo % 16 == 0 && lds >= 0,
+             "hn_dequantize_rows: row strides must cover the rows and be multiples of 16 elements");
+  HN_REQUIRE(out_dtype >= HN_DTYPE_BF16 && out_dtype <= HN_DTYPE_F32, "hn_dequantize_rows: bad out dtype %d", out_dtype);
+  HN_REQUIRE(q && s && out, "hn_dequantize_rows: null pointer");
+  HN_REQUIRE(aligned16(q) && aligned16(out), "hn_dequantize_rows: codes and output must be 16-byte aligned");
+  if (rows == 0) return HN_OK;
+  const int64_t cpr = D / 16, n = rows * cpr;
+  HN_REQUIRE(cpr <= 0x7fffffff && (n + 255) / 256 <= 0x7fffffff, "hn_dequantize_rows: too large");
+  const unsigned blocks = (unsigned)((n + 255) / 256);
+  hipStream_t st = (hipStream_t)stream;
+#define HN_DQ(DT, WIDE)                                                                                          \
+  hipLaunchKernelGGL((dequant_rows_kernel<DT, WIDE>), dim3(blocks), dim3(256), 0, st, q, ldq, s, lds, rows, (int)cpr, \
+                     out, ldo)
+  const bool wide = (int64_t)blocks * 256 > 0xffffffffLL;
+  if (out_dtype == HN_DTYPE_BF16) { if (wide) HN_DQ(HN_DTYPE_BF16, true); else HN_DQ(HN_DTYPE_BF16, false); }
+  else if (out_dtype == HN_DTYPE_F16) { if (wide) HN_DQ(HN_DTYPE_F16, true); else HN_DQ(HN_DTYPE_F16, false); }
+  else { if (wide) HN_DQ(HN_DTYPE_F32, true); else HN_DQ(HN_DTYPE_F32, false); }
+#undef HN_DQ
+  return HN_LAUNCH_CHECK("dequant_rows_kernel");
 }
 
 extern "C" int hn_qk_norm_rope(const void* x, int64_t ldx, const float* weight, const float* cos_t, const float* sin_t,

@@ -109,6 +109,17 @@ int hn_gated_residual(const void* x, const void* y, const void* gate, int dtype,
                       int64_t D, void* out, void* stream);
 
 /*
+ * Row-scaled int8 dequantization.  Replaces world.dequantize_kv (hy_nomas/world.py:93-94):
+ *   out[r, :] = out_dtype(float(q[r, :]) * s[r * lds]), the fp32 product rounded once, then to out_dtype.
+ *   q [rows, D] int8 (row stride ldq), s fp32 (lds = 1 for [rows, 1]), out [rows, D] (row stride ldo).
+ *   D % 16 == 0; q, out 16-byte aligned; row strides multiples of 16 elements.  The matching quantizer
+ *   (world.quantize_kv, world.py:83-90: absmax per token and head, half away from zero) is
+ *   hn_quantize_act with group = D.
+ */
+int hn_dequantize_rows(const int8_t* q, int64_t ldq, const float* s, int64_t lds, int64_t rows, int64_t D,
+                       void* out, int out_dtype, int64_t ldo, void* stream);
+
+/*
  * Per-head RMSNorm + interleaved RoPE.  Replaces fused.qk_norm_rope / _qk_norm_rope_kernel
  * (hy_nomas/fused.py:65-105).
  *   x [B, L, H, D] bf16 with token stride ldx (heads contiguous, batch stride L * ldx), weight [D] fp32

@@ -125,6 +125,19 @@ def quantize(x, group=128, kind="int8", rounding="half_away"):
     return q, s
 
 
+def quantize_kv(x):
+    """hy_nomas/world.py:83-90: x [L, H, D] -> (int8 [L, H, D], fp32 [L, H, 1]), one group per (token, head)."""
+    x = to_f32(x)
+    l, h, d = x.shape
+    q, s = quantize(x.reshape(l * h, d), d)
+    return q.reshape(l, h, d), s.reshape(l, h, 1)
+
+
+def dequantize_kv(q, s):
+    """hy_nomas/world.py:93-94 to bf16: fp32 product of code and scale, rounded once, then to bf16."""
+    return rbf16(np.asarray(q, dtype=np.float32) * _f32(s))
+
+
 def quantize_g128(w):
     """hy_nomas/ops.py:41-52 weight quantization (K padded up to a multiple of 128 with zeros)."""
     w = to_f32(w)

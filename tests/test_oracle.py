@@ -102,6 +102,27 @@ def test_quantize_zero_group_and_g128_weights():
     assert np.array_equal(q2.numpy(), qo2) and np.array_equal(s2.numpy(), so2)
 
 
+def test_kv_quant_matches_reference_torch_form():
+    """world.py:83-94 restated with torch ops (absmax per (token, head), IEEE division, floor/ceil half away,
+    clamp; dequant as an fp32 product then bf16) against the oracle, with forced ties and an all-zero head."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(37, 5, 128, generator=g) * 3).to(torch.bfloat16).float()
+    x[3, 2] = 0.0                                     # all-zero head: scale 1, codes 0
+    x[4, 1, :] = torch.arange(128, dtype=torch.float32) - 63.5   # peak 64 -> scale 64/127: no tie by design
+    x[5, 0, :] = 0.0
+    x[5, 0, 0] = 127.0                                # scale exactly 1: the next values are exact ties
+    x[5, 0, 1:9] = torch.tensor([0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5])
+    peak = x.abs().amax(dim=-1, keepdim=True)
+    scale = torch.where(peak > 0, peak / 127.0, torch.ones_like(peak))
+    scaled = x / scale
+    ref_q = torch.where(scaled >= 0, torch.floor(scaled + 0.5), torch.ceil(scaled - 0.5)).clamp_(-127, 127)
+    q, s = oracle.quantize_kv(x.numpy())
+    assert np.array_equal(q, ref_q.to(torch.int8).numpy()) and np.array_equal(s, scale.numpy())
+    assert q[5, 0, 1:9].tolist() == [1, -1, 2, -2, 3, -3, 127, -127]
+    ref_dq = (torch.from_numpy(q).float() * torch.from_numpy(s)).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oracle.dequantize_kv(q, s), ref_dq)
+
+
 def test_fast_division_lemma_exhaustive():
     """Every bf16 absmax >= 2^-80 and every bf16 x with |x| <= absmax, both signs: the device's reciprocal +
     FMA quotient with unclamped rounding gives the same int8 codes (half away from zero and half to even) as
