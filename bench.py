@@ -148,6 +148,39 @@ def linear_stack_with_quant(dev, gen, steps, warmup):
     return ms
 
 
+def decoder_mlp(dev, gen, steps, warmup):
+    """PixelUMM decoder MLP on fp8 block weights at the reference's kernel-bench shape (M=35200 tokens,
+    hidden 4096, intermediate 12288): down(silu(gate(x)) * up(x)).  "fused": x quantized once, gate and up
+    in one GEMM whose epilogue writes the e4m3 codes of the SwiGLU product, then the down GEMM.
+    "unfused": the reference's order (three fp8 linears, torch's bf16 silu and product)."""
+    from hy_nomas import kernels, pixelumm
+
+    m, hid, inter = 35200, 4096, 12288
+    x = outlier_activations(m, hid, gen, dev)
+    ws = {}
+    for name, (o, k) in {"gate": (inter, hid), "up": (inter, hid), "down": (hid, inter)}.items():
+        ws[name] = pixelumm.quantize_fp8_block(torch.randn(o, k, generator=gen, device=dev) * 0.02)
+    gate_up = pixelumm.interleave_gate_up(ws["gate"], ws["up"])
+    fused = [lambda: pixelumm.swiglu_mlp(x, gate_up, ws["down"])]
+    lin = pixelumm.fp8_block_linear
+    unfused = [lambda: lin(torch.nn.functional.silu(lin(x, *ws["gate"])) * lin(x, *ws["up"]), *ws["down"])]
+    ops = 2 * m * hid * inter * 3
+    out = {"M": m, "hidden": hid, "intermediate": inter}
+    for name, fns in (("fused", fused), ("unfused", unfused)):
+        ms, _ = time_launches(fns, steps, warmup, WARM_S)
+        out[name] = {"ms": round(ms, 4), "TFLOPS": round(ops / (ms * 1e-3) / 1e12, 1)}
+    # the fused path's two GEMMs alone, per launch
+    qa, sa = kernels.quantize_activations(x, "fp8")
+    hq, hs = kernels.block_gemm(qa, sa, *gate_up, kind="fp8", epilogue="swiglu_quant")
+    _, per = time_launches([lambda: kernels.block_gemm(qa, sa, *gate_up, kind="fp8", epilogue="swiglu_quant"),
+                            lambda: kernels.block_gemm(hq, hs, *ws["down"], kind="fp8")], steps, warmup)
+    out["gate_up_swiglu_gemm"] = {"ms": round(per[0], 4), "TFLOPS": round(2 * m * hid * 2 * inter / (per[0] * 1e-3) / 1e12, 1)}
+    out["down_gemm"] = {"ms": round(per[1], 4), "TFLOPS": round(2 * m * inter * hid / (per[1] * 1e-3) / 1e12, 1)}
+    del x, ws, gate_up, qa, sa, hq, hs, fused, unfused
+    torch.cuda.empty_cache()
+    return out
+
+
 def kv_history(dev, gen, steps, warmup):
     """int8 K/V history of the config-4 block: K [57344, 24, 128] bf16, quantized per (token, head) and
     dequantized back to bf16, two rotating slabs (> the 256 MB Infinity Cache together with their codes)."""
@@ -320,6 +353,7 @@ def main():
         ms_f, per_f, ops = gemm_stack(dev, gen, args.steps, args.warmup, kind="fp8")
         print(json.dumps({"fp8_block_gemm_stack_ms": round(ms_f, 4), "per_gemm_ms": [round(t, 4) for t in per_f],
                           "TFLOPS": round(ops / (ms_f * 1e-3) / 1e12, 1)}))
+        print(json.dumps({"decoder_mlp_fp8": decoder_mlp(dev, gen, args.steps, args.warmup)}))
         return
     if args.only == "g128":
         ms_g, per_g, ops = gemm_stack(dev, gen, args.steps, args.warmup, group_mode="g128")
@@ -381,6 +415,8 @@ def main():
             fp8[name] = {"ms": round(t, 4), "TFLOPS": round(2 * M * n * k / (t * 1e-3) / 1e12, 1)}
         extra["fp8_block_gemm"] = {"per_gemm": fp8, "stack_ms": round(ms_f, 4),
                                    "frac_fp8_peak": round(ops / (ms_f * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 3)}
+        log("bench: decoder MLP (fp8, fused SwiGLU)")
+        extra["decoder_mlp_fp8"] = decoder_mlp(dev, gen, max(5, args.steps // 2), 2)
         log("bench: elementwise")
         extra["elementwise"] = elementwise(dev, gen, max(10, args.steps), 3)
         log("bench: kv history")

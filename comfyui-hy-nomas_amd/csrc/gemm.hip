@@ -42,15 +42,24 @@ template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
   // fp8 with block weight scales rescales its running sum in place (no second accumulator set), so it
   // fits the 256 x 256 tile
-  if (g128 && a.sw_rows == 128)
-    return launch_cfg<KIND, EPI, true, 2, 4, 4, KIND == HN_KIND_FP8 ? 2 : 1, OUT_DT, 128, 2, true>(a, st);
-  if (g128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
-  return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+  // swiglu_quant splits each wave's tokens between the gate and up waves, so it needs two token blocks
+  // per wave (TM = 2): the per-token tile, or fp8 with block weight scales
+  constexpr bool SWIGLU = EPI == HN_EPI_SWIGLU_QUANT;
+  if (g128 && a.sw_rows == 128) {
+    if constexpr (!SWIGLU || KIND == HN_KIND_FP8)
+      return launch_cfg<KIND, EPI, true, 2, 4, 4, KIND == HN_KIND_FP8 ? 2 : 1, OUT_DT, 128, 2, true>(a, st);
+  } else if (g128) {
+    if constexpr (!SWIGLU) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
+  } else {
+    return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+  }
+  set_error("hn_block_gemm: swiglu_quant needs per-token scales or fp8 with 128 x 128 block weight scales");
+  return HN_ERR_UNSUPPORTED;
 }
 
 template <int KIND, int EPI>
 static int launch_out(GemmArgs& a, bool g128, int out_dtype, hipStream_t st) {
-  if constexpr (EPI == HN_EPI_GELU_QUANT || EPI == HN_EPI_ACC32) {
+  if constexpr (EPI == HN_EPI_GELU_QUANT || EPI == HN_EPI_ACC32 || EPI == HN_EPI_SWIGLU_QUANT) {
     return launch_group<KIND, EPI, HN_DTYPE_BF16>(a, g128, st);
   } else {
     if (out_dtype == HN_DTYPE_BF16) return launch_group<KIND, EPI, HN_DTYPE_BF16>(a, g128, st);
@@ -65,6 +74,7 @@ static int launch_kind(GemmArgs& a, bool g128, int epilogue, int out_dtype, hipS
     case HN_EPI_NONE: return launch_out<KIND, HN_EPI_NONE>(a, g128, out_dtype, st);
     case HN_EPI_GELU: return launch_out<KIND, HN_EPI_GELU>(a, g128, out_dtype, st);
     case HN_EPI_GELU_QUANT: return launch_out<KIND, HN_EPI_GELU_QUANT>(a, g128, out_dtype, st);
+    case HN_EPI_SWIGLU_QUANT: return launch_out<KIND, HN_EPI_SWIGLU_QUANT>(a, g128, out_dtype, st);
     default: break;
   }
   set_error("hn_block_gemm: bad epilogue %d", epilogue);
@@ -83,14 +93,21 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   HN_REQUIRE(K % 128 == 0, "hn_block_gemm: K=%lld is not a multiple of 128", (long long)K);
   HN_REQUIRE(group == 128 || group == K, "hn_block_gemm: group must be 128 or K (got %lld)", (long long)group);
   HN_REQUIRE(kind == HN_KIND_INT8 || kind == HN_KIND_FP8, "hn_block_gemm: bad kind %d", kind);
-  HN_REQUIRE(epilogue >= HN_EPI_NONE && epilogue <= HN_EPI_ACC32, "hn_block_gemm: bad epilogue %d", epilogue);
+  HN_REQUIRE(epilogue >= HN_EPI_NONE && epilogue <= HN_EPI_SWIGLU_QUANT, "hn_block_gemm: bad epilogue %d", epilogue);
   HN_REQUIRE(epilogue != HN_EPI_ACC32 || kind == HN_KIND_INT8, "hn_block_gemm: ACC32 is int8 only");
   HN_REQUIRE(epilogue != HN_EPI_GELU_QUANT || (N % 128 == 0 && qs != nullptr && ldqs >= N / 128),
              "hn_block_gemm: gelu_quant needs N %% 128 == 0 and qs [M, N/128]");
   HN_REQUIRE(out_dtype >= HN_DTYPE_BF16 && out_dtype <= HN_DTYPE_F32, "hn_block_gemm: bad out dtype %d", out_dtype);
   HN_REQUIRE(bias == nullptr || (bias_dtype >= HN_DTYPE_BF16 && bias_dtype <= HN_DTYPE_F32),
              "hn_block_gemm: bad bias dtype %d", bias_dtype);
-  HN_REQUIRE(lda >= K && ldw >= K && ldo >= N, "hn_block_gemm: row strides smaller than the rows");
+  HN_REQUIRE(epilogue != HN_EPI_SWIGLU_QUANT || (N % 256 == 0 && qs != nullptr && ldqs >= N / 256),
+             "hn_block_gemm: swiglu_quant needs N %% 256 == 0 (gate and up interleaved in 128-row blocks) and "
+             "qs [M, N/256]");
+  HN_REQUIRE((epilogue != HN_EPI_GELU_QUANT && epilogue != HN_EPI_SWIGLU_QUANT) ||
+                 (ldo % 4 == 0 && ((uintptr_t)out & 3) == 0),
+             "hn_block_gemm: quantized outputs are stored 4 codes at a time: ldo %% 4 == 0, 4-byte aligned out");
+  HN_REQUIRE(lda >= K && ldw >= K && ldo >= (epilogue == HN_EPI_SWIGLU_QUANT ? N / 2 : N),
+             "hn_block_gemm: row strides smaller than the rows");
   HN_REQUIRE(lda % 16 == 0 && ldw % 16 == 0, "hn_block_gemm: code row strides must be multiples of 16 bytes");
   HN_REQUIRE(lda < (1 << 22) && ldw < (1 << 22) && ldsa < (1 << 22) && ldsw < (1 << 22) && ldo < (1 << 22),
              "hn_block_gemm: row strides must be below 2^22 elements");

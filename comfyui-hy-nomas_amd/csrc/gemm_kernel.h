@@ -83,6 +83,10 @@ __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) 
   return ((const float*)bias)[n];
 }
 
+// torch's silu of a bf16 value, computed in fp32 as x / (1 + exp(-x)) (the reference's F.silu,
+// hy_nomas/pixelumm.py:322, on a bf16 tensor)
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // kernels.py:74-77, fp32, evaluated in the order written
   float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
@@ -204,6 +208,10 @@ void block_gemm_kernel(const GemmArgs a) {
   static_assert(SLICES >= 2 && SLICES % 2 == 0, "fragment sets alternate per slice, starting each stage at set 0");
   static_assert(kGroupK % BK == 0, "stage size");
   static_assert(EPI != HN_EPI_GELU_QUANT || TN * 32 == 128, "gelu_quant needs a 128-channel wave tile");
+  // swiglu_quant: wave wn = 0 holds gate rows and wn = 1 the up rows of the same 128 MLP channels (the
+  // weight interleaves them in 128-row blocks), and each finishes half of the wave's tokens
+  static_assert(EPI != HN_EPI_SWIGLU_QUANT || (WN == 2 && TN * 32 == 128 && TM % 2 == 0),
+                "swiglu_quant needs two 128-channel waves per tile row and an even token split");
   // WBLK: one weight-scale row per 128 output channels (the fp8 128 x 128 block layout); a wave's TN * 32
   // channels then lie in one block, so the group fold multiplies by one scale product per token
   static_assert(!WBLK || (G128 && (TN * 32) % 128 == 0 && BN % 128 == 0), "block weight scales");
@@ -221,7 +229,10 @@ void block_gemm_kernel(const GemmArgs a) {
   constexpr int OPITCH = TN * 32 * 2 + 16;
   constexpr int STG_OFF = SCR + STAGE;
   constexpr int RING_END = SCR + NS * STAGE;
-  constexpr int STG_END = STG_OFF + (STAGED ? NW * 32 * OPITCH : 0);
+  // swiglu_quant hands half of each wave's bf16 outputs to its partner wave through the same area
+  constexpr int XCH_WAVE = EPI == HN_EPI_SWIGLU_QUANT ? (TM / 2) * TN * 32 * 32 * 2 : 0;
+  constexpr int STG_BYTES = STAGED ? NW * 32 * OPITCH : NW * XCH_WAVE;
+  constexpr int STG_END = STG_OFF + STG_BYTES;
   constexpr int EP_OFF = STG_END > RING_END ? STG_END : RING_END;
   constexpr int EP_BYTES = EPI == HN_EPI_ACC32 ? 0 : (2 * BN + BM) * 4;  // sw | bias | sa of the tile
   constexpr int SMEM = EP_OFF + EP_BYTES > RING_END ? EP_OFF + EP_BYTES : RING_END;
@@ -575,6 +586,112 @@ void block_gemm_kernel(const GemmArgs a) {
             }
         }
       }
+    } else if constexpr (EPI == HN_EPI_SWIGLU_QUANT) {
+      // per-channel bias and per-token scale of this tile (written at the tile top)
+      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF);
+      constexpr int JH = TM / 2;
+      // every output of the wave to its bf16 value: gate_proj(x) on wave wn = 0, up_proj(x) on wn = 1
+#pragma unroll
+      for (int j = 0; j < TM; j++) {
+        const float sam = G128 ? 0.0f : ep[2 * BN + erow_m + j * 32];
+#pragma unroll
+        for (int i = 0; i < TN; i++) {
+#pragma unroll
+          for (int rr = 0; rr < 4; rr++) {
+            const float4 sw4 = *reinterpret_cast<const float4*>(ep + nloc + i * 32 + rr * 8);
+            const float4 b4 = *reinterpret_cast<const float4*>(ep + BN + nloc + i * 32 + rr * 8);
+            const float swq[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
+            const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const int r = rr * 4 + q;
+              float v;
+              if constexpr (RESCALE) v = MF::get(acc[i][j], r) * ss_last[j];
+              else if constexpr (G128) v = facc[i][j][r];
+              else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
+              MF::put(acc[i][j], r, rbf16(v + bq[q]));
+            }
+          }
+        }
+      }
+      // The partner wave (wave ^ 1) holds the other operand of every product in the same lane and
+      // register.  Each wave writes the token half it does not finish (wn = 0 finishes j < JH, wn = 1 the
+      // rest) as packed bf16 pairs: 16 bytes per lane per 8 registers, lane-contiguous, conflict-free.
+      auto send = [&](auto jc) __attribute__((always_inline)) {
+        constexpr int J0 = decltype(jc)::value;
+        char* slot = smem + STG_OFF + wave * XCH_WAVE + tl * 16;
+#pragma unroll
+        for (int jj = 0; jj < JH; jj++)
+#pragma unroll
+          for (int i = 0; i < TN; i++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+              uint32_t w[4];
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                w[e] = __builtin_amdgcn_perm(__float_as_uint(MF::get(acc[i][J0 + jj], h * 8 + 2 * e + 1)),
+                                             __float_as_uint(MF::get(acc[i][J0 + jj], h * 8 + 2 * e)), 0x07060302u);
+              *reinterpret_cast<v4i*>(slot + ((jj * TN + i) * 2 + h) * 1024) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            }
+      };
+      if (wn == 0) send(std::integral_constant<int, JH>());
+      else send(std::integral_constant<int, 0>());
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      barrier();
+      // h = bf16(bf16(silu(g)) * u), then the codes of each token's 128-channel group (lanes l and l^32)
+      auto finish = [&](auto jc, auto gate_c) __attribute__((always_inline)) {
+        constexpr int J0 = decltype(jc)::value;
+        constexpr bool OWN_GATE = decltype(gate_c)::value;
+        const char* pslot = smem + STG_OFF + (wave ^ 1) * XCH_WAVE + tl * 16;
+#pragma unroll
+        for (int jj = 0; jj < JH; jj++) {
+          const int j = J0 + jj;
+          float peak = 0.0f;
+#pragma unroll
+          for (int i = 0; i < TN; i++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+              const v4i p = *reinterpret_cast<const v4i*>(pslot + ((jj * TN + i) * 2 + h) * 1024);
+#pragma unroll
+              for (int e = 0; e < 8; e++) {
+                const int r = h * 8 + e;
+                const uint32_t pw = (uint32_t)p[e >> 1];
+                const float other = __uint_as_float((e & 1) ? (pw & 0xffff0000u) : (pw << 16));
+                const float own = MF::get(acc[i][J0 + jj], r);
+                const float g = OWN_GATE ? own : other, u = OWN_GATE ? other : own;
+                const float hv = rbf16(rbf16(silu_f32(g)) * u);
+                MF::put(acc[i][J0 + jj], r, hv);
+                peak = __builtin_fmaxf(peak, __builtin_fabsf(hv));
+              }
+            }
+          peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));
+          const float gs = KIND == HN_KIND_FP8 ? fp8_scale(peak) : int8_scale(peak);
+          const bool fast = fast_group(peak);  // h holds bf16 values: the exact three-op quotient applies
+          const FastDiv<KIND == HN_KIND_FP8> div(gs);
+          const int ml = erow_m + j * 32;
+          if (ml < mrem) {
+            uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + em0 * a.ldo + en0 / 2;
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int rr = 0; rr < 4; rr++) {
+                const int nl = (tl >> 5) * 4 + i * 32 + rr * 8;
+                int c[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                  const float v = MF::get(acc[i][J0 + jj], rr * 4 + q);
+                  const float y = __builtin_expect(fast, 1) ? div(v) : v / gs;
+                  if constexpr (KIND == HN_KIND_FP8) c[q] = (int)e4m3_encode(y);
+                  else c[q] = round_half_away_i8(y);
+                }
+                *reinterpret_cast<uint32_t*>(o + (uint32_t)(ml * (int)a.ldo + nl)) = pack4_i8(c[0], c[1], c[2], c[3]);
+              }
+            if (tl < 32) a.qs[(em0 + ml) * a.ldqs + en0 / 256] = gs;
+          }
+        }
+      };
+      if (wn == 0) finish(std::integral_constant<int, 0>(), std::true_type());
+      else finish(std::integral_constant<int, JH>(), std::false_type());
     } else {
       // per-channel scale and bias, and per-token scale, of this tile (written at the tile top)
       const float* ep = reinterpret_cast<const float*>(smem + EP_OFF);

@@ -16,7 +16,7 @@ import torch
 from . import _lib
 
 GROUP = 128
-EPILOGUES = {None: 0, "gelu": 1, "gelu_quant": 2}
+EPILOGUES = {None: 0, "gelu": 1, "gelu_quant": 2, "swiglu_quant": 4}
 
 
 def _aligned(t, bytes_):
@@ -64,19 +64,30 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
     """Block-scaled GEMM on quantized activations (hy_nomas/kernels.py:152-170).  With epilogue
     "gelu_quant" returns (int8 [M, N], scales [M, N / 128]) ready for the next int8 linear; otherwise
     [M, N] in `out_dtype`.  Weight scales are [N, K/128] or [N, 1] (one row per output channel), or
-    [ceil(N/128), K/128]: one row per 128 output channels (the fp8 128 x 128 block layout)."""
+    [ceil(N/128), K/128]: one row per 128 output channels (the fp8 128 x 128 block layout).
+
+    "swiglu_quant" (the decoder MLP, hy_nomas/pixelumm.py:314-323): qw holds the gate and up weights
+    interleaved in 128-row blocks (`pixelumm.interleave_gate_up`); returns the codes of
+    bf16(silu(gate) * up) in this GEMM's kind, [M, N / 2], and their scales [M, N / 256], ready for the
+    down projection.  Needs per-token scales, or fp8 with block weight scales."""
     _lib.require_device(qa, sa, qw, sw, bias)
     m, k = qa.shape
     n = qw.shape[0]
     mode = EPILOGUES[epilogue]
+    quantized = mode in (2, 4)
     if mode == 2:
         out = torch.empty((m, n), device=qa.device, dtype=torch.int8)
         qs = torch.empty((m, n // GROUP), device=qa.device, dtype=torch.float32)
+    elif mode == 4:
+        if n % (2 * GROUP):
+            raise RuntimeError(f"swiglu_quant: {n} weight rows are not whole gate/up block pairs of {2 * GROUP}")
+        out = torch.empty((m, n // 2), device=qa.device, dtype=torch.int8 if kind == "int8" else torch.float8_e4m3fn)
+        qs = torch.empty((m, n // (2 * GROUP)), device=qa.device, dtype=torch.float32)
     else:
         out = torch.empty((m, n), device=qa.device, dtype=out_dtype)
         qs = None
     if m == 0:
-        return (out, qs) if mode == 2 else out
+        return (out, qs) if quantized else out
     # weight scales with one row per channel, or one row per 128 channels (block layout, g128 fold only)
     sw_rows = 1 if sw.shape[0] == n else GROUP
     if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
@@ -94,9 +105,9 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
         bias = bias.contiguous()
     _lib.call("hn_block_gemm", qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
               sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
-              m, n, k, group, _lib.KIND[kind], mode, out.data_ptr(), _lib.dtype_code(out) if mode != 2 else 0,
+              m, n, k, group, _lib.KIND[kind], mode, out.data_ptr(), 0 if quantized else _lib.dtype_code(out),
               out.stride(0), _lib.ptr(qs), qs.stride(0) if qs is not None else 0, _lib.stream(qa))
-    return (out, qs) if mode == 2 else out
+    return (out, qs) if quantized else out
 
 
 def block_gemm_acc32(qa, qw):

@@ -34,8 +34,9 @@ enum hn_kind { HN_KIND_INT8 = 0, HN_KIND_FP8 = 1 };
 /* int8 rounding of x / scale: half away from zero (the reference's rule), or half to even */
 enum hn_round { HN_ROUND_HALF_AWAY = 0, HN_ROUND_HALF_EVEN = 1 };
 
-/* GEMM epilogues (kernels.py:149 EPILOGUES) plus a raw int32 accumulator output for testing */
-enum hn_epilogue { HN_EPI_NONE = 0, HN_EPI_GELU = 1, HN_EPI_GELU_QUANT = 2, HN_EPI_ACC32 = 3 };
+/* GEMM epilogues (kernels.py:149 EPILOGUES), a raw int32 accumulator output for testing, and the SwiGLU
+ * product of the PixelUMM decoder MLP requantized for its down projection */
+enum hn_epilogue { HN_EPI_NONE = 0, HN_EPI_GELU = 1, HN_EPI_GELU_QUANT = 2, HN_EPI_ACC32 = 3, HN_EPI_SWIGLU_QUANT = 4 };
 
 /* row normalisation of the adaLN kernels: LayerNorm without affine (the reference), or RMSNorm */
 enum hn_norm { HN_NORM_LAYER = 0, HN_NORM_RMS = 1 };
@@ -76,6 +77,14 @@ int hn_quantize_act(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * GELU_QUANT: out int8 [M, N] codes of the GELU output, quantized per row and 128 columns, with scales
  * qs [M, N / 128] (kernels.py:129-137); N % 128 == 0.  ACC32: out int32 [M, N] = full-K integer dot
  * products (int8 only; a test hook, scales and bias are ignored).
+ * SWIGLU_QUANT: the decoder MLP's down_proj input, down_proj(silu(gate_proj(x)) * up_proj(x))
+ * (hy_nomas/pixelumm.py:314-323), from one GEMM over the gate and up weights.  qw [N, K] holds them
+ * interleaved in 128-row blocks: rows 256 b .. 256 b + 127 are gate rows 128 b .., the next 128 rows the
+ * up rows 128 b .. (sw, and bias if given, interleaved the same way).  With g = bf16(gate output) and
+ * u = bf16(up output), h = bf16(bf16(g / (1 + exp(-g))) * u) (torch's bf16 silu and product) is quantized
+ * per row and 128 columns like hn_quantize_act with this GEMM's kind: out [M, N / 2] codes (int8 or e4m3,
+ * row stride ldo), qs [M, N / 256] fp32.  N % 256 == 0; per-token scales (group == K), or fp8 with
+ * sw_rows == 128.
  * K % 128 == 0; M, N >= 1.
  */
 int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,

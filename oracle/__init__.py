@@ -19,6 +19,7 @@ Reference functions restated (reference-tree file:line):
   pixelumm_qk       hy_nomas/fused.py:131-186
   fp8 weight blocks hy_nomas/pixelumm.py:60-82
   dequant_linear    hy_nomas/ops.py:167-176 (the reference's CPU fallback: dequantize + F.linear)
+  swiglu            hy_nomas/pixelumm.py:314-323 (the decoder MLP's silu(gate) * up on bf16 tensors)
 """
 import ctypes
 import os
@@ -69,6 +70,9 @@ def lib():
     l.hno_e4m3_decode.restype = ctypes.c_float
     l.hno_gelu_tanh.argtypes = [ctypes.c_float]
     l.hno_gelu_tanh.restype = ctypes.c_float
+    l.hno_silu.argtypes = [ctypes.c_float]
+    l.hno_silu.restype = ctypes.c_float
+    l.hno_swiglu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i64, ctypes.c_void_p]
     l.hno_check_fast_division.argtypes = [ctypes.c_int, _i64, _i64]
     l.hno_check_fast_division.restype = ctypes.c_int64
     l.hno_check_scale_division.argtypes = []
@@ -177,6 +181,25 @@ def block_gemm(qa, sa, qw, sw, bias=None, kind="int8", epilogue=None, want_acc32
                          _p(out), _p(qout), _p(qs), _p(acc))
     res = (qout, qs, out) if epilogue == "gelu_quant" else out
     return (res, acc) if want_acc32 else res
+
+
+def swiglu(g, u):
+    """h = rbf16(rbf16(silu(g)) * u) for bf16-valued g, u (hy_nomas/pixelumm.py:322): the down_proj input of
+    the decoder MLP.  Returns fp32 arrays holding bf16 values."""
+    g = _f32(g)
+    u = _f32(u)
+    assert g.shape == u.shape
+    h = np.empty_like(g)
+    lib().hno_swiglu(_p(g), _p(u), g.size, _p(h))
+    return h
+
+
+def swiglu_quant(g, u, kind="fp8"):
+    """The swiglu product quantized per row and 128 columns, as the down projection's activation
+    quantizer does (pixelumm.py:152 -> kernels.py:22-54): (codes, scales, h)."""
+    h = swiglu(g, u)
+    q, s = quantize(h, 128, kind)
+    return q, s, h
 
 
 def adaln(x, shift, scale, eps=1e-6, norm="layer", quant=False, rounding="half_away"):

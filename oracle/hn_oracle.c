@@ -21,6 +21,7 @@
  *   hy_nomas/fused.py:108-118   _gated_residual_kernel     -> hno_gated_residual
  *   hy_nomas/fused.py:131-175   _pixelumm_qk_kernel        -> hno_pixelumm_qk
  *   hy_nomas/ops.py:41-62       quantize_g128/dequantize   -> hno_quantize (group 128)
+ *   hy_nomas/pixelumm.py:322    MLP silu(gate) * up        -> hno_swiglu
  */
 #include <math.h>
 #include <stdint.h>
@@ -147,6 +148,16 @@ static inline float gelu_tanh(float x) {
 }
 
 float hno_gelu_tanh(float x) { return gelu_tanh(x); }
+
+/* pixelumm.py:322, F.silu(gate) * up on bf16 tensors: silu in fp32 as x / (1 + exp(-x)), rounded to
+ * bf16, then the bf16 product (exact in fp32) rounded to bf16. */
+static inline float silu(float x) { return x / (1.0f + expf(-x)); }
+
+float hno_silu(float x) { return silu(x); }
+
+void hno_swiglu(const float* g, const float* u, int64_t n, float* h) {
+    for (int64_t i = 0; i < n; i++) h[i] = rbf16(rbf16(silu(g[i])) * u[i]);
+}
 
 /* kernels.py:80-137.  For each output element, group by group in order:
  *     acc = fma(part_g * sa[m, g], sb[n, g], acc)

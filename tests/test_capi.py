@@ -61,3 +61,9 @@ def test_argument_validation_without_a_gpu():
     rc = l.hn_block_gemm(None, 256, None, 1, None, 256, None, 1, 128, None, 0, 4, 8, 256, 256, 1, 0, None, 0, 8, None,
                          0, None)   # block weight scales need group 128
     assert rc == 1 and b"sw_rows" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 128, None, 0, 4, 384, 256, 128, 1, 4, None, 0, 192,
+                         None, 1, None)   # swiglu_quant over 384 rows: not whole gate/up pairs of 256
+    assert rc == 1 and b"swiglu_quant" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 128, None, 0, 4, 512, 256, 128, 1, 4, None, 0, 256,
+                         None, 1, None)   # swiglu_quant scales [M, N/256] missing
+    assert rc == 1 and b"swiglu_quant" in l.hn_last_error()

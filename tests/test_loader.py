@@ -120,3 +120,70 @@ def test_block_from_checkpoint_runs_on_the_int8_path(dev, tmp_path):
         ri, rt = block.reference_double_stream(blk.img, blk.txt, img, txt, img_mods, txt_mods, rope)
     for got, ref in ((gi, ri), (gt, rt)):
         assert ((got.float() - ref).norm() / ref.norm()).item() < 2e-2
+
+
+def test_pixelumm_fp8_checkpoint_round_trip_and_gate_up_interleave(tmp_path):
+    """The decoder's single-file FP8 format (hy_nomas/pixelumm.py:35, 470-485): fp8_weight / fp8_scale pairs
+    under decoder.*, detected by metadata or keys; the fused gate/up weight alternates 128-row blocks."""
+    from safetensors.torch import save_file
+
+    from hy_nomas import pixelumm
+
+    g = seeded(11)
+    sd = {"layers.0.mlp.gate_proj.weight": torch.randn(384, 256, generator=g) * 0.02,
+          "layers.0.mlp.up_proj.weight": torch.randn(384, 256, generator=g) * 0.02,
+          "layers.0.mlp.down_proj.weight": torch.randn(256, 384, generator=g) * 0.02,
+          "layers.0.input_norm.weight": torch.rand(256, generator=g) + 0.5,
+          "head.linear.bias": torch.randn(100, generator=g)}
+    fp8 = pixelumm.fp8_state_dict(sd)
+    assert fp8["layers.0.mlp.gate_proj.fp8_weight"].dtype == torch.float8_e4m3fn
+    assert fp8["layers.0.mlp.gate_proj.fp8_scale"].shape == (3, 2)
+    assert fp8["layers.0.input_norm.weight"].dtype == torch.bfloat16
+    path = os.path.join(tmp_path, "decoder_fp8.safetensors")
+    save_file({"decoder." + k: v for k, v in fp8.items()} | {"dcae.enc.weight": torch.zeros(2)}, path,
+              metadata={"format": pixelumm.FP8_FORMAT})
+    state, is_fp8 = pixelumm.load_state_dict(path)
+    assert is_fp8 and set(state) == set(fp8)
+    assert torch.equal(state["layers.0.mlp.up_proj.fp8_weight"].view(torch.uint8),
+                       fp8["layers.0.mlp.up_proj.fp8_weight"].view(torch.uint8))
+    bf_path = os.path.join(tmp_path, "decoder_bf16.safetensors")
+    save_file({"decoder." + k: v.to(torch.bfloat16) for k, v in sd.items()}, bf_path)
+    assert pixelumm.load_state_dict(bf_path)[1] is False
+    with pytest.raises(ValueError):
+        save_file({"other.weight": torch.zeros(2)}, os.path.join(tmp_path, "x.safetensors"))
+        pixelumm.load_state_dict(os.path.join(tmp_path, "x.safetensors"))
+    # dequantized fp8 blocks stay within the e4m3 step of the weights
+    w = sd["layers.0.mlp.gate_proj.weight"]
+    wd = pixelumm.dequantize_fp8_block(fp8["layers.0.mlp.gate_proj.fp8_weight"],
+                                       fp8["layers.0.mlp.gate_proj.fp8_scale"], torch.float32)
+    assert ((wd - w).abs().max() / w.abs().max()).item() < 2 ** -3
+    gate = (fp8["layers.0.mlp.gate_proj.fp8_weight"], fp8["layers.0.mlp.gate_proj.fp8_scale"])
+    up = (fp8["layers.0.mlp.up_proj.fp8_weight"], fp8["layers.0.mlp.up_proj.fp8_scale"])
+    q, s = pixelumm.interleave_gate_up(gate, up)
+    assert q.shape == (768, 256) and s.shape == (6, 2) and q.dtype == torch.float8_e4m3fn
+    for b in range(3):
+        assert torch.equal(q[256 * b:256 * b + 128].view(torch.uint8), gate[0][128 * b:128 * (b + 1)].view(torch.uint8))
+        assert torch.equal(q[256 * b + 128:256 * (b + 1)].view(torch.uint8), up[0][128 * b:128 * (b + 1)].view(torch.uint8))
+        assert torch.equal(s[2 * b], gate[1][b]) and torch.equal(s[2 * b + 1], up[1][b])
+
+
+def test_decoder_mlp_dequant_path_is_the_reference_expression():
+    """pixelumm.MLP with matmul="dequant" (CPU): down_proj(F.silu(gate_proj(x)) * up_proj(x)) on the
+    dequantized bf16 weights (hy_nomas/pixelumm.py:314-323, 150-155)."""
+    from hy_nomas import pixelumm
+
+    g = seeded(12)
+    arch = pixelumm.Arch(hidden_size=256, intermediate_size=384)
+    mlp = pixelumm.MLP(arch, pixelumm.DecoderOps.with_matmul("dequant"))
+    sd = {}
+    for name, (o, k) in {"gate_proj": (384, 256), "up_proj": (384, 256), "down_proj": (256, 384)}.items():
+        q, s = pixelumm.quantize_fp8_block(torch.randn(o, k, generator=g) * 0.03)
+        sd[f"{name}.fp8_weight"], sd[f"{name}.fp8_scale"] = q, s
+    mlp.load_state_dict(sd, strict=False)
+    x = torch.randn(5, 256, generator=g).to(torch.bfloat16)
+    wd = {n: pixelumm.dequantize_fp8_block(sd[f"{n}.fp8_weight"], sd[f"{n}.fp8_scale"], torch.bfloat16)
+          for n in ("gate_proj", "up_proj", "down_proj")}
+    ref = torch.nn.functional.linear(
+        torch.nn.functional.silu(torch.nn.functional.linear(x, wd["gate_proj"])) *
+        torch.nn.functional.linear(x, wd["up_proj"]), wd["down_proj"])
+    assert torch.equal(mlp(x), ref)

@@ -382,3 +382,27 @@ def test_exact_rational_rounding_agrees_except_fp32_quirk():
             assert float(np.float32(abs(yi)) + np.float32(0.5)) == abs(qi)
             quirk += 1
     assert quirk <= 2
+
+
+def test_swiglu_silu_matches_torch_bf16_and_float64_for_every_bf16():
+    """oracle.swiglu's silu (pixelumm.py:322, F.silu on a bf16 tensor): for every finite bf16 g, with u = 1,
+    h equals torch's CPU bf16 silu, and equals the float64 silu rounded to bf16 wherever exp(-g) is finite in
+    fp32 (below -88.7 the fp32 formula gives -0, as torch's does).  Then the product rounding: h(g, u) for
+    random bf16 u equals rbf16(h(g, 1) * u), the exact product rounded once."""
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint32)
+    g = (bits << 16).view(np.float32)
+    g = g[np.isfinite(g)]
+    h = oracle.swiglu(g, np.ones_like(g))
+    t = torch.nn.functional.silu(torch.from_numpy(g).to(torch.bfloat16)).float().numpy()
+    assert np.array_equal(h.view(np.uint32), t.view(np.uint32))
+    ok = g > -88.5
+    g64 = g[ok].astype(np.float64)
+    exact = g64 / (1.0 + np.exp(-g64))
+    assert np.array_equal(h[ok], oracle.rbf16(exact.astype(np.float32)))
+    rng = np.random.default_rng(3)
+    u = oracle.rbf16(rng.standard_normal(g.size).astype(np.float32) * 4)
+    h2 = oracle.swiglu(g, u)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(h2, oracle.rbf16(h * u))
