@@ -181,6 +181,32 @@ def decoder_mlp(dev, gen, steps, warmup):
     return out
 
 
+def modulation_linear(dev, gen, steps, warmup):
+    """The per-sample modulation linear of a double-stream block (hy_nomas/model.py:306-314): silu(vec)
+    [B, 3072] -> [B, 18432] with Tencent's int8 g128 weight, at B = 1 and 2: the skinny int8 kernel,
+    bound by the 56.6 MB weight stream.  Eight weight copies rotate (453 MB > the Infinity Cache)."""
+    from hy_nomas import kernels
+
+    k, n = HIDDEN, 6 * HIDDEN
+    ws = []
+    for _ in range(8):
+        w = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+        sw = torch.rand(n, k // 128, generator=gen, device=dev) * 4e-3 + 1e-3
+        ws.append((w, sw.float(), (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)))
+    nbytes = n * k + n * (k // 128) * 4
+    out = {"N": n, "K": k, "weight_bytes": nbytes}
+    for b in (1, 2):
+        qa, sa = kernels.quantize_activations(torch.randn(b, k, generator=gen, device=dev).to(torch.bfloat16))
+        fns = [lambda w=w: kernels.block_gemm(qa, sa, w[0], w[1], w[2]) for w in ws]
+        total_ms, _ = time_launches(fns, steps, warmup)
+        us = 1e3 * total_ms / len(fns)
+        out[f"B{b}"] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                        "frac_hbm": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 3)}
+    del ws
+    torch.cuda.empty_cache()
+    return out
+
+
 def kv_history(dev, gen, steps, warmup):
     """int8 K/V history of the config-4 block: K [57344, 24, 128] bf16, quantized per (token, head) and
     dequantized back to bf16, two rotating slabs (> the 256 MB Infinity Cache together with their codes)."""
@@ -217,9 +243,12 @@ def elementwise(dev, gen, steps, warmup):
     shift = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
     scale = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
     gate = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    # camera output per latent frame: 32 frames of 1024 tokens
+    frames = (torch.randn(1, 32, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
     cases = {
         "adaln": (lambda s: fused.adaln(s[0], shift, scale), 4.0),
         "gated_residual": (lambda s: fused.gated_residual(s[0], s[1], gate), 6.0),
+        "gated_residual_frames": (lambda s: fused.gated_residual_frames(s[0], s[1], gate, frames), 6.0),
         "adaln_quant": (lambda s: kernels.adaln_quant(s[0], shift, scale), 3.0 + 4.0 / 128),
         "quantize_g128": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN)), 3.0 + 4.0 / 128),
         "quantize_per_token": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN), "int8", None),
@@ -314,7 +343,49 @@ def cpu_baseline(target_s=20.0):
     ops = sum(2 * rows * n * k for _, k, n in STACK)
     return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": f"{rows} token rows of each of the 4 GEMMs (M=32768 full), median of {reps}, "
-                      f"{dt:.2f} s per pass; dequantize_g128 + bf16 F.linear"}
+                      f"{dt:.2f} s per pass; dequantize_g128 + bf16 F.linear",
+            "also": cpu_restatements(threads)}
+
+
+def cpu_restatements(threads):
+    """The W8A8 arithmetic of the path restated on the CPU, timed beside the fallback: the oracle's int8
+    g128 GEMM at 1024 x 3072 -> 3072 (19.3 G ops), its g128 activation quantizer, and the torch forms of
+    adaLN and the gated residual at [1, 32768, 3072] (median of 3 each)."""
+    import oracle
+
+    g = torch.Generator().manual_seed(1)
+
+    def med(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[reps // 2]
+
+    m, k, n = 1024, HIDDEN, HIDDEN
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    qa, sa = oracle.quantize(x)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).numpy()
+    sw = (torch.rand(n, k // 128, generator=g) * 4e-3 + 1e-3).numpy()
+    t_gemm = med(lambda: oracle.block_gemm(qa, sa, w, sw))
+    big = torch.randn(1, M, HIDDEN, generator=g).to(torch.bfloat16)
+    y = torch.randn(1, M, HIDDEN, generator=g).to(torch.bfloat16)
+    shift = (torch.randn(1, HIDDEN, generator=g) * 0.1).to(torch.bfloat16)
+    scale = (torch.randn(1, HIDDEN, generator=g) * 0.1).to(torch.bfloat16)
+    gate = (torch.randn(1, HIDDEN, generator=g) * 0.1).to(torch.bfloat16)
+    t_quant = med(lambda: oracle.quantize(big.view(M, HIDDEN)), 1)
+    t_adaln = med(lambda: (torch.nn.functional.layer_norm(big.float(), (HIDDEN,), eps=1e-6)
+                           * (1 + scale.float()).to(torch.bfloat16).float()[:, None] + shift.float()[:, None])
+                  .to(torch.bfloat16))
+    t_gr = med(lambda: big + y * gate[:, None])
+    n_el = M * HIDDEN
+    return {"threads": threads,
+            "w8a8_oracle_gemm_1024x3072x3072": {"s": round(t_gemm, 3), "TOPS": round(2 * m * n * k / t_gemm / 1e12, 4)},
+            "quantize_g128_oracle_GBps": round(n_el * (3 + 4 / 128) / t_quant / 1e9, 2),
+            "adaln_torch_GBps": round(n_el * 4 / t_adaln / 1e9, 2),
+            "gated_residual_torch_GBps": round(n_el * 6 / t_gr / 1e9, 2)}
 
 
 def main():
@@ -363,6 +434,7 @@ def main():
     if args.only == "elementwise":
         print(json.dumps(elementwise(dev, gen, max(10, args.steps), 3)))
         print(json.dumps(kv_history(dev, gen, max(10, args.steps), 3)))
+        print(json.dumps({"modulation_linear": modulation_linear(dev, gen, max(10, args.steps), 3)}))
         return
     if args.block_only:
         with torch.no_grad():
@@ -421,6 +493,8 @@ def main():
         extra["elementwise"] = elementwise(dev, gen, max(10, args.steps), 3)
         log("bench: kv history")
         extra["kv_history"] = kv_history(dev, gen, max(10, args.steps), 3)
+        log("bench: modulation linear (M = batch)")
+        extra["modulation_linear"] = modulation_linear(dev, gen, max(10, args.steps), 3)
         for pt in (True, False):
             name = "dit_block_M57344_" + ("per_token" if pt else "g128")
             log("bench: " + name)

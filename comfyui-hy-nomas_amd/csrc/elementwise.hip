@@ -294,10 +294,14 @@ static int adaln_norm(int norm, const void* x, const void* shift, const void* sc
 // integer division per element; the batch of a row is computed once per wave.
 constexpr int kGrRows = 4;
 
-template <int DT>
+// FRAMES: the camera module's per-frame output is then added (hy_nomas/model.py:518-520): token r of
+// [B, T * P] tokens belongs to frame row r / P of frame [B, T, D]; the sum is rounded to the dtype before
+// the add, as the reference's two tensor operations do.
+template <int DT, bool FRAMES>
 __global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ yv,
                                                              const uint16_t* __restrict__ gate,
+                                                             const uint16_t* __restrict__ frame, int64_t P,
                                                              uint16_t* __restrict__ out, int64_t rows, int64_t L,
                                                              int cpr) {
   const int c = blockIdx.x * 64 + threadIdx.x;
@@ -308,14 +312,20 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __r
     const uint4 xv = *reinterpret_cast<const uint4*>(x + r * D + c * 8);
     const uint4 yy = *reinterpret_cast<const uint4*>(yv + r * D + c * 8);
     const uint4 gv = *reinterpret_cast<const uint4*>(gate + b * D + c * 8);
-    float a[8], bb[8], g[8], o[8];
+    float a[8], bb[8], g[8], o[8], fr[8];
     widen8<DT>(xv, a);
     widen8<DT>(yy, bb);
     widen8<DT>(gv, g);
+    if constexpr (FRAMES) widen8<DT>(*reinterpret_cast<const uint4*>(frame + (r / P) * D + c * 8), fr);
     bool nan = false;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
       o[j] = a[j] + round_to<DT>(bb[j] * g[j]);
+      if constexpr (FRAMES) {
+        float s = round_to<DT>(o[j]);
+        asm volatile("" : "+v"(s));  // rounded on its own, never fused into the add below
+        o[j] = s + fr[j];
+      }
       nan |= o[j] != o[j];
     }
     uint4 packed;
@@ -325,9 +335,9 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __r
   }
 }
 
-template <int DT>
+template <int DT, bool FRAMES = false>
 static int launch_gated_residual(const void* x, const void* y, const void* gate, int64_t rows, int64_t L, int64_t D,
-                                 void* out, hipStream_t st) {
+                                 void* out, hipStream_t st, const void* frame = nullptr, int64_t P = 1) {
   const int64_t cpr = D / 8;
   if (cpr > 0x7fffffff) {
     set_error("hn_gated_residual: D too large");
@@ -336,9 +346,9 @@ static int launch_gated_residual(const void* x, const void* y, const void* gate,
   const int64_t gx = (cpr + 63) / 64;
   int64_t gy = (rows + kGrRows - 1) / kGrRows;
   gy = gy > 65535 ? 65535 : gy;
-  hipLaunchKernelGGL((gated_residual_kernel<DT>), dim3((unsigned)gx, (unsigned)gy), dim3(64, kGrRows), 0, st,
-                     (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)gate, (uint16_t*)out, rows, L,
-                     (int)cpr);
+  hipLaunchKernelGGL((gated_residual_kernel<DT, FRAMES>), dim3((unsigned)gx, (unsigned)gy), dim3(64, kGrRows), 0,
+                     st, (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)gate, (const uint16_t*)frame, P,
+                     (uint16_t*)out, rows, L, (int)cpr);
   return HN_LAUNCH_CHECK("gated_residual_kernel");
 }
 
@@ -553,6 +563,23 @@ extern "C" int hn_gated_residual(const void* x, const void* y, const void* gate,
   if (dtype == HN_DTYPE_BF16) return launch_gated_residual<HN_DTYPE_BF16>(x, y, gate, B * L, L, D, out, st);
   if (dtype == HN_DTYPE_F16) return launch_gated_residual<HN_DTYPE_F16>(x, y, gate, B * L, L, D, out, st);
   set_error("hn_gated_residual: unsupported dtype %d", dtype);
+  return HN_ERR_UNSUPPORTED;
+}
+
+extern "C" int hn_gated_residual_frames(const void* x, const void* y, const void* gate, const void* frame, int dtype,
+                                        int64_t B, int64_t T, int64_t P, int64_t D, void* out, void* stream) {
+  HN_REQUIRE(B >= 0 && T >= 0 && P > 0 && D > 0, "hn_gated_residual_frames: bad shape");
+  HN_REQUIRE(D % 8 == 0, "hn_gated_residual_frames: D=%lld must be a multiple of 8", (long long)D);
+  HN_REQUIRE(x && y && gate && frame && out, "hn_gated_residual_frames: null pointer");
+  HN_REQUIRE(aligned16(x) && aligned16(y) && aligned16(gate) && aligned16(frame) && aligned16(out),
+             "hn_gated_residual_frames: pointers must be 16-byte aligned");
+  if (B * T == 0) return HN_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == HN_DTYPE_BF16)
+    return launch_gated_residual<HN_DTYPE_BF16, true>(x, y, gate, B * T * P, T * P, D, out, st, frame, P);
+  if (dtype == HN_DTYPE_F16)
+    return launch_gated_residual<HN_DTYPE_F16, true>(x, y, gate, B * T * P, T * P, D, out, st, frame, P);
+  set_error("hn_gated_residual_frames: unsupported dtype %d", dtype);
   return HN_ERR_UNSUPPORTED;
 }
 

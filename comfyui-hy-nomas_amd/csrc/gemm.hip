@@ -1,6 +1,7 @@
 // Dispatch and C ABI of the block-scaled 8-bit GEMM (hy_nomas/kernels.py:152-170, block_gemm).
 // The kernel template and its design notes are in gemm_kernel.h.
 #include "gemm_kernel.h"
+#include "skinny_kernel.h"
 
 namespace hn {
 
@@ -81,6 +82,35 @@ static int launch_kind(GemmArgs& a, bool g128, int epilogue, int out_dtype, hipS
   return HN_ERR_ARG;
 }
 
+// M <= 4 int8 (the per-sample linears): one wave per 4 weight rows, v_dot4 on the streamed weights.
+template <int MT, int MODE, int EPI>
+static int launch_skinny_out(GemmArgs& a, int out_dtype, hipStream_t st) {
+  constexpr int64_t ROWS = kSkinnyRows * kSkinnyWaves;
+  const int64_t grid = (a.N + ROWS - 1) / ROWS;
+  if (grid > 0x7fffffff) {
+    set_error("hn_block_gemm: problem too large (N=%lld)", (long long)a.N);
+    return HN_ERR_UNSUPPORTED;
+  }
+  const dim3 g((unsigned)grid), b(kSkinnyWaves * 64);
+  if (out_dtype == HN_DTYPE_BF16) hipLaunchKernelGGL((skinny_gemm_kernel<MT, MODE, EPI, HN_DTYPE_BF16>), g, b, 0, st, a);
+  else if (out_dtype == HN_DTYPE_F16) hipLaunchKernelGGL((skinny_gemm_kernel<MT, MODE, EPI, HN_DTYPE_F16>), g, b, 0, st, a);
+  else hipLaunchKernelGGL((skinny_gemm_kernel<MT, MODE, EPI, HN_DTYPE_F32>), g, b, 0, st, a);
+  return HN_LAUNCH_CHECK("skinny_gemm_kernel");
+}
+
+template <int MT, int MODE>
+static int launch_skinny_epi(GemmArgs& a, int epilogue, int out_dtype, hipStream_t st) {
+  if (epilogue == HN_EPI_GELU) return launch_skinny_out<MT, MODE, HN_EPI_GELU>(a, out_dtype, st);
+  return launch_skinny_out<MT, MODE, HN_EPI_NONE>(a, out_dtype, st);
+}
+
+template <int MODE>
+static int launch_skinny_mode(GemmArgs& a, int epilogue, int out_dtype, hipStream_t st) {
+  if (a.M == 1) return launch_skinny_epi<1, MODE>(a, epilogue, out_dtype, st);
+  if (a.M == 2) return launch_skinny_epi<2, MODE>(a, epilogue, out_dtype, st);
+  return launch_skinny_epi<4, MODE>(a, epilogue, out_dtype, st);
+}
+
 }  // namespace hn
 
 extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
@@ -133,6 +163,11 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   // per-token mode also serves a single-group K == 128 problem with one scale row per channel
   const bool g128 = group == 128 && (K != 128 || sw_rows == 128);
   if (epilogue == HN_EPI_ACC32) return launch_group<HN_KIND_INT8, HN_EPI_ACC32, HN_DTYPE_BF16>(a, false, st);
+  if (kind == HN_KIND_INT8 && M <= kSkinnyMaxM && (epilogue == HN_EPI_NONE || epilogue == HN_EPI_GELU)) {
+    if (!g128) return launch_skinny_mode<0>(a, epilogue, out_dtype, st);
+    if (sw_rows == 128) return launch_skinny_mode<2>(a, epilogue, out_dtype, st);
+    return launch_skinny_mode<1>(a, epilogue, out_dtype, st);
+  }
   if (kind == HN_KIND_INT8) return launch_kind<HN_KIND_INT8>(a, g128, epilogue, out_dtype, st);
   return launch_kind<HN_KIND_FP8>(a, g128, epilogue, out_dtype, st);
 }

@@ -305,7 +305,9 @@ void block_gemm_kernel(const GemmArgs a) {
         scbase[u] = a.sa + m0 * a.ldsa;
         scoff[u] = (uint32_t)min((q - BN / 64) * 64 + lane, mlim) * (uint32_t)a.ldsa;
       } else {
-        scbase[u] = a.sw + n0 * a.ldsw;
+        // weight-scale row 0: it exists in both scale layouts (with block scales, sw has only
+        // ceil(N / 128) rows, so row n0 may lie past the end)
+        scbase[u] = a.sw;
         scoff[u] = 0;
       }
     }

@@ -80,6 +80,28 @@ def gated_residual(x, y, gate):
     return out
 
 
+def gated_residual_frames(x, y, gate, frame):
+    """gated_residual(x, y, gate) followed by the camera module's per-frame add in one pass
+    (hy_nomas/model.py:518-520): x, y [B, T * P, D], gate [B, D], frame [B, T, D] (or [1, T, D], broadcast
+    over the batch) -> (gated_residual(x, y, gate).view(B, T, P, D) + frame[:, :, None]).view(B, T * P, D),
+    with the same two roundings."""
+    _lib.require_device(x, y, gate, frame)
+    b, l, d = x.shape
+    t = frame.shape[1]
+    if frame.shape[0] not in (1, b) or frame.shape[2] != d or t == 0 or l % t:
+        raise RuntimeError(f"gated_residual_frames: frame {tuple(frame.shape)} does not tile x {tuple(x.shape)}")
+    x = x.contiguous()
+    y = y.contiguous()
+    gate = gate.to(x.dtype).contiguous()
+    frame = frame.to(x.dtype).expand(b, t, d).contiguous()
+    out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    if b * l == 0:
+        return out
+    _lib.call("hn_gated_residual_frames", x.data_ptr(), y.data_ptr(), gate.data_ptr(), frame.data_ptr(),
+              _lib.dtype_code(x), b, t, l // t, d, out.data_ptr(), _lib.stream(x))
+    return out
+
+
 def pixelumm_qk(x, weight_t, weight_hw, cos, sin, eps=1e-6):
     """x [1, N, H, D] (a projection's output, heads contiguous), cos/sin [N, D] fp32 -> bf16 [1, N, H, D]
     (hy_nomas/fused.py:178-186)."""

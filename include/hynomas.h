@@ -118,6 +118,16 @@ int hn_gated_residual(const void* x, const void* y, const void* gate, int dtype,
                       int64_t D, void* out, void* stream);
 
 /*
+ * Gated residual, then the camera module's per-frame output added to every token of its frame: the end
+ * of a double-stream block's image side plus the broadcast add after it (hy_nomas/model.py:275-284 with
+ * hy_nomas/model.py:518-520), in one pass.
+ *   out = dtype(dtype(x + bf16(y * gate[b])) + frame[b, t]) for token p of frame t:
+ *   x, y, out [B, T * P, D] contiguous, gate [B, D], frame [B, T, D] contiguous, all of dtype.
+ */
+int hn_gated_residual_frames(const void* x, const void* y, const void* gate, const void* frame, int dtype,
+                             int64_t B, int64_t T, int64_t P, int64_t D, void* out, void* stream);
+
+/*
  * Row-scaled int8 dequantization.  Replaces world.dequantize_kv (hy_nomas/world.py:93-94):
  *   out[r, :] = out_dtype(float(q[r, :]) * s[r * lds]), the fp32 product rounded once, then to out_dtype.
  *   q [rows, D] int8 (row stride ldq), s fp32 (lds = 1 for [rows, 1]), out [rows, D] (row stride ldo).

@@ -161,3 +161,23 @@ def test_adaln_quant_per_token(dev, b, l, d):
     q_ref, s_ref = oracle.quantize(y, d)
     assert (q.cpu().numpy() != q_ref).mean() < 1e-3
     assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,t,p,d,frame_b", [(1, 3, 5, 3072, 1), (2, 4, 33, 256, 2), (2, 2, 7, 64, 1)])
+def test_gated_residual_frames_matches_two_torch_ops(dev, dtype, b, t, p, d, frame_b):
+    """The block's last gated residual and the camera module's per-frame add (hy_nomas/model.py:518-520)
+    in one pass: bit-exact against gated_residual followed by torch's broadcast add."""
+    from hy_nomas import fused
+
+    print(f"gated_residual_frames {dtype} b={b} t={t} p={p} d={d}", flush=True)
+    g = seeded(b * 100 + t * 10 + p + d)
+    x = (torch.randn(b, t * p, d, generator=g) * 3).to(dtype).to(dev)
+    y = torch.randn(b, t * p, d, generator=g).to(dtype).to(dev)
+    gate = (torch.randn(b, d, generator=g) * 0.3).to(dtype).to(dev)
+    frame = (torch.randn(frame_b, t, d, generator=g) * 0.5).to(dtype).to(dev)
+    got = fused.gated_residual_frames(x, y, gate, frame)
+    ref = (fused.gated_residual(x, y, gate).view(b, t, p, d) + frame.unsqueeze(2)).view(b, t * p, d)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    with pytest.raises(RuntimeError):
+        fused.gated_residual_frames(x, y, gate, frame[:, :1].expand(frame_b, t + 1, d)[:, : t + 1])

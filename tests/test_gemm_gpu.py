@@ -233,3 +233,59 @@ def test_fp8_block_linear(dev):
                                      bias.float())
     assert got.shape == (3, 170, 768)
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 3e-2
+
+
+@pytest.mark.parametrize("layout", ["g128", "per_token", "block"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", [(18432, 3072), (200, 640), (3072, 12288)])
+def test_skinny_m_equals_the_tile_kernel(dev, layout, m, n, k):
+    """M <= 4 int8 runs the skinny v_dot4 kernel (the per-sample linears, e.g. the modulation linear
+    3072 -> 18432 at batch 1-2).  Its rows must equal, bit for bit, the same rows of a large-M product
+    (the MFMA tile kernel), for every scale layout, with a ragged N and a K that ends mid-step."""
+    from hy_nomas import kernels
+
+    print(f"skinny {layout} m={m} n={n} k={k}", flush=True)
+    g = seeded(m * 7 + n + k)
+    x = outlier_input(300, k, m * 7 + n + k)
+    group = None if layout == "per_token" else 128
+    qa, sa = kernels.quantize_activations(x.to(dev), "int8", group)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+    if layout == "per_token":
+        sw = (torch.rand(n, 1, generator=g) * 4e-3 + 1e-3).to(dev)
+    elif layout == "g128":
+        sw = (torch.rand(n, k // 128, generator=g) * 4e-3 + 1e-3).to(dev)
+    else:
+        sw = (torch.rand((n + 127) // 128, k // 128, generator=g) * 4e-3 + 1e-3).to(dev)
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    for out_dtype, epi in ((torch.bfloat16, None), (torch.float32, None), (torch.bfloat16, "gelu"),
+                           (torch.float16, None)):
+        big = kernels.block_gemm(qa, sa, w, sw, bias, out_dtype, epilogue=epi)
+        small = kernels.block_gemm(qa[:m].clone(), sa[:m].clone(), w, sw, bias, out_dtype, epilogue=epi)
+        assert small.shape == (m, n)
+        assert torch.equal(small.view(torch.int16) if out_dtype != torch.float32 else small,
+                           big[:m].view(torch.int16) if out_dtype != torch.float32 else big[:m])
+    nob = kernels.block_gemm(qa[:m].clone(), sa[:m].clone(), w, sw, None, torch.float32)
+    assert torch.equal(nob, kernels.block_gemm(qa, sa, w, sw, None, torch.float32)[:m])
+    if layout != "block" and n == 200:
+        ref = oracle.block_gemm(qa[:m].cpu().numpy(), sa[:m].cpu().numpy(), w.cpu().numpy(), sw.cpu().numpy(),
+                                oracle.to_f32(bias.cpu()))
+        got = kernels.block_gemm(qa[:m].clone(), sa[:m].clone(), w, sw, bias, torch.float32).cpu().numpy()
+        assert np.array_equal(got, ref)
+
+
+def test_modulation_linear_from_silu_vec(dev):
+    """The reference's Modulate (hy_nomas/model.py:306-314): linear(silu(vec)) with an int8 g128 weight at
+    batch 1, through block_linear (quantize + skinny GEMM), vs the dequantized fp32 product."""
+    from hy_nomas import kernels, ops
+
+    print("modulation linear", flush=True)
+    g = seeded(99)
+    vec = torch.randn(1, 3072, generator=g).to(torch.bfloat16)
+    w = torch.randn(6 * 3072, 3072, generator=g) * 0.02
+    q, s = ops.quantize_g128(w)
+    bias = (torch.randn(6 * 3072, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.nn.functional.silu(vec.to(dev))
+    got = kernels.block_linear(x, q.to(dev), s.to(dev), bias.to(dev))
+    ref = torch.nn.functional.linear(x.float().cpu(), ops.dequantize_g128(q, s, torch.float32), bias.float())
+    assert got.shape == (1, 18432)
+    assert ((got.float().cpu() - ref).norm() / ref.norm()).item() < 2e-2
