@@ -171,3 +171,45 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   if (kind == HN_KIND_INT8) return launch_kind<HN_KIND_INT8>(a, g128, epilogue, out_dtype, st);
   return launch_kind<HN_KIND_FP8>(a, g128, epilogue, out_dtype, st);
 }
+
+extern "C" int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                            const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
+                            int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
+                            const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
+                            int64_t L_total, int64_t l_offset, void* stream) {
+  using namespace hn;
+  HN_REQUIRE(B >= 0 && L >= 0 && hidden > 0 && K > 0, "hn_qkv_heads: bad shape");
+  HN_REQUIRE(hidden % 128 == 0, "hn_qkv_heads: hidden=%lld is not a multiple of the head dim 128", (long long)hidden);
+  HN_REQUIRE(K % 128 == 0, "hn_qkv_heads: K=%lld is not a multiple of 128", (long long)K);
+  HN_REQUIRE(group == 128 || group == K, "hn_qkv_heads: group must be 128 or K (got %lld)", (long long)group);
+  HN_REQUIRE(kind == HN_KIND_INT8 || kind == HN_KIND_FP8, "hn_qkv_heads: bad kind %d", kind);
+  HN_REQUIRE(sw_rows == 1 || (sw_rows == 128 && group == 128), "hn_qkv_heads: sw_rows must be 1, or 128 with group 128");
+  HN_REQUIRE(l_offset >= 0 && L_total >= l_offset + L, "hn_qkv_heads: tokens [%lld, %lld) exceed L_total=%lld",
+             (long long)l_offset, (long long)(l_offset + L), (long long)L_total);
+  HN_REQUIRE(B * L < ((int64_t)1 << 31), "hn_qkv_heads: B * L must be below 2^31");
+  HN_REQUIRE(lda >= K && ldw >= K && lda % 16 == 0 && ldw % 16 == 0, "hn_qkv_heads: bad code row strides");
+  HN_REQUIRE(lda < (1 << 22) && ldw < (1 << 22) && ldsa < (1 << 22) && ldsw < (1 << 22),
+             "hn_qkv_heads: row strides must be below 2^22 elements");
+  HN_REQUIRE(ldsa >= K / group && ldsw >= K / group, "hn_qkv_heads: scale row strides too small");
+  HN_REQUIRE(bias == nullptr || (bias_dtype >= HN_DTYPE_BF16 && bias_dtype <= HN_DTYPE_F32), "hn_qkv_heads: bad bias dtype");
+  HN_REQUIRE(qa && sa && qw && sw && q_norm_w && k_norm_w && out, "hn_qkv_heads: null pointer");
+  HN_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), "hn_qkv_heads: cos and sin must both be given or both NULL");
+  HN_REQUIRE(((uintptr_t)qa & 15) == 0 && ((uintptr_t)qw & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
+                 ((uintptr_t)q_norm_w & 15) == 0 && ((uintptr_t)k_norm_w & 15) == 0 &&
+                 ((uintptr_t)cos_t & 15) == 0 && ((uintptr_t)sin_t & 15) == 0,
+             "hn_qkv_heads: codes, output, norm weights and rope tables must be 16-byte aligned");
+  if (B * L == 0) return HN_OK;
+  GemmArgs a{};
+  a.qa = (const uint8_t*)qa; a.lda = lda; a.sa = sa; a.ldsa = ldsa;
+  a.qw = (const uint8_t*)qw; a.ldw = ldw; a.sw = sw; a.ldsw = ldsw; a.sw_rows = (int)sw_rows;
+  a.bias = bias; a.bias_dtype = bias_dtype;
+  a.M = B * L; a.N = 3 * hidden; a.K = K;
+  a.out = out; a.ldo = 3 * hidden;
+  a.stage_store = 1;
+  a.hm_L = L; a.hm_Ltot = L_total; a.hm_loff = l_offset; a.hm_hidden = hidden; a.hm_B = B;
+  a.hm_wq = q_norm_w; a.hm_wk = k_norm_w; a.hm_cos = cos_t; a.hm_sin = sin_t; a.hm_eps = eps;
+  hipStream_t st = (hipStream_t)stream;
+  const bool g128 = group == 128 && (K != 128 || sw_rows == 128);
+  if (kind == HN_KIND_INT8) return launch_group<HN_KIND_INT8, kEpiQkvHeads, HN_DTYPE_BF16>(a, g128, st);
+  return launch_group<HN_KIND_FP8, kEpiQkvHeads, HN_DTYPE_BF16>(a, g128, st);
+}

@@ -57,7 +57,19 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int vec_store;    // out rows 8-byte aligned and N % 4 == 0
   int stage_store;  // 2-byte out with 16-byte aligned rows and N % 8 == 0: LDS-staged 16-byte stores
+  // kEpiQkvHeads: the QKV projection of hidden = N / 3 channels, rows m = b * hm_L + l, written head-major
+  // to out [3, hm_B, hidden / 128, hm_Ltot, 128] at token hm_loff + l; q and k RMS-normalized per head
+  // with weights hm_wq / hm_wk ([128] fp32), then rotated by hm_cos / hm_sin ([hm_L, 128] fp32) if given
+  int64_t hm_L, hm_Ltot, hm_loff, hm_hidden, hm_B;
+  const float* hm_wq;
+  const float* hm_wk;
+  const float* hm_cos;
+  const float* hm_sin;
+  float hm_eps;
 };
+
+// Internal epilogue id of the head-major QKV projection (entry point hn_qkv_heads).
+constexpr int kEpiQkvHeads = 5;
 
 constexpr int kGroupK = 128;  // bytes of K per scale group (the g128 layout)
 constexpr int kGroupM = 8;    // token tiles per column group in the tile order
@@ -225,7 +237,10 @@ void block_gemm_kernel(const GemmArgs a) {
   // lanes along N.  The staging area lies past stage buffer 0 (which holds the next tile's first stage).
   // The tile's epilogue operands (per-channel scales and bias, per-token scales) are written at the tile
   // top, while stage buffer 1 fills, so they lie past both the staging area and the stage ring.
-  constexpr bool STAGED = OUT_DT != HN_DTYPE_F32 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU);
+  constexpr bool STAGED =
+      OUT_DT != HN_DTYPE_F32 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU || EPI == kEpiQkvHeads);
+  static_assert(EPI != kEpiQkvHeads || (TN * 32 == 128 && OUT_DT == HN_DTYPE_BF16),
+                "head-major QKV: one 128-channel head per wave, bf16 out");
   constexpr int OPITCH = TN * 32 * 2 + 16;
   constexpr int STG_OFF = SCR + STAGE;
   constexpr int RING_END = SCR + NS * STAGE;
@@ -724,6 +739,51 @@ void block_gemm_kernel(const GemmArgs a) {
             }
           }
         }
+        if constexpr (EPI == kEpiQkvHeads) {
+          // q and k heads (hy_nomas/fused.py:65-91 on the bf16 projection output): r = 1/sqrt(mean(x^2) + eps)
+          // over the head's 128 channels (lanes l and l^32 hold them), n = bf16(bf16(x r) w), then the
+          // interleaved rotation of the pairs (2i, 2i + 1), which lie in one lane
+          const int64_t c0 = en0 + wn * 128;
+          const int part = (int)(c0 / a.hm_hidden);
+          if (part < 2) {
+            const float* wt = part == 0 ? a.hm_wq : a.hm_wk;
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int r = 0; r < 16; r++) {
+                const float xv = rbf16(MF::get(acc[i][j], r));
+                MF::put(acc[i][j], r, xv);
+                ss = __builtin_fmaf(xv, xv, ss);
+              }
+            ss += shfl_xor_f(ss, 32);
+            const float rs = 1.0f / __builtin_sqrtf(ss / 128.0f + a.hm_eps);
+            const uint32_t mg = (uint32_t)(em0 + (ml < mrem ? ml : mrem - 1));
+            const uint32_t tok = mg % (uint32_t)a.hm_L;
+            const bool rope = a.hm_cos != nullptr;
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int rr = 0; rr < 4; rr++) {
+                const int d = i * 32 + rr * 8 + (tl >> 5) * 4;
+                const float4 w4 = *reinterpret_cast<const float4*>(wt + d);
+                float nq[4];
+                nq[0] = rbf16(rbf16(MF::get(acc[i][j], rr * 4 + 0) * rs) * w4.x);
+                nq[1] = rbf16(rbf16(MF::get(acc[i][j], rr * 4 + 1) * rs) * w4.y);
+                nq[2] = rbf16(rbf16(MF::get(acc[i][j], rr * 4 + 2) * rs) * w4.z);
+                nq[3] = rbf16(rbf16(MF::get(acc[i][j], rr * 4 + 3) * rs) * w4.w);
+                if (rope) {
+                  const float4 c4 = *reinterpret_cast<const float4*>(a.hm_cos + (int64_t)tok * 128 + d);
+                  const float4 s4 = *reinterpret_cast<const float4*>(a.hm_sin + (int64_t)tok * 128 + d);
+                  const float o0 = nq[0] * c4.x - nq[1] * s4.x, o1 = nq[1] * c4.y + nq[0] * s4.y;
+                  const float o2 = nq[2] * c4.z - nq[3] * s4.z, o3 = nq[3] * c4.w + nq[2] * s4.w;
+                  nq[0] = o0; nq[1] = o1; nq[2] = o2; nq[3] = o3;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; q++) MF::put(acc[i][j], rr * 4 + q, nq[q]);
+              }
+          }
+        }
         if constexpr (EPI == HN_EPI_GELU_QUANT) {
           // the wave's TN*32 = 128 channels are one group: lanes l and l^32 hold them for token m
           float peak = 0.0f;
@@ -757,7 +817,7 @@ void block_gemm_kernel(const GemmArgs a) {
             // N % 128 == 0, so the group is either wholly inside N or wholly past it
             if (tl < 32 && wn * 128 < nrem) a.qs[(em0 + ml) * a.ldqs + (en0 + wn * 128) / 128] = gs;
           }
-        } else if (STAGED && a.stage_store) {
+        } else if (STAGED && (EPI == kEpiQkvHeads || a.stage_store)) {
           // token row (tl & 31) of this wave's staging block, then a 16-byte-per-lane write-back of the
           // block's 32 rows x TN*32 channels, non-temporal so the output stream does not evict the operand
           // panels other tiles are still reading from L2
@@ -776,13 +836,28 @@ void block_gemm_kernel(const GemmArgs a) {
           __builtin_amdgcn_wave_barrier();
           constexpr int LPR = TN * 32 * 2 / 16, RPI = 64 / LPR;  // lanes per token row, rows per instruction
           uint16_t* obase = reinterpret_cast<uint16_t*>(a.out) + em0 * a.ldo + en0;
+          // head-major QKV: the wave's head (part, h) block of out, rows at token hm_loff + l of batch b
+          uint16_t* hbase = nullptr;
+          if constexpr (EPI == kEpiQkvHeads) {
+            const int64_t c0 = en0 + wn * 128;
+            const int64_t part = c0 / a.hm_hidden, h = (c0 % a.hm_hidden) / 128;
+            hbase = reinterpret_cast<uint16_t*>(a.out) + (part * a.hm_B * (a.hm_hidden / 128) + h) * a.hm_Ltot * 128;
+          }
 #pragma unroll
           for (int r0 = 0; r0 < 32; r0 += RPI) {
             const int orow = r0 + tl / LPR, ocol = (tl % LPR) * 8;
             const v4i v = *reinterpret_cast<const v4i*>(wst + orow * OPITCH + ocol * 2);
             const int ml2 = wm * TM * 32 + j * 32 + orow, nl = wn * TN * 32 + ocol;
-            if (ml2 < mrem && nl < nrem)
-              __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(obase + (uint32_t)(ml2 * (int)a.ldo + nl)));
+            if (ml2 < mrem && nl < nrem) {
+              if constexpr (EPI == kEpiQkvHeads) {
+                const uint32_t mg = (uint32_t)(em0 + ml2);
+                const uint32_t bb = mg / (uint32_t)a.hm_L, ll = mg - bb * (uint32_t)a.hm_L;
+                uint16_t* o = hbase + ((int64_t)bb * (a.hm_hidden / 128) * a.hm_Ltot + a.hm_loff + ll) * 128 + ocol;
+                __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(o));
+              } else {
+                __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(obase + (uint32_t)(ml2 * (int)a.ldo + nl)));
+              }
+            }
           }
         } else if (m_ok) {
 #pragma unroll

@@ -104,6 +104,14 @@ class DiTBlockInt8:
         v = qkv[:, :, 2]
         return q, k, v
 
+    def attention_heads(self, x, shift1, scale1, rope=None, out=None, l_offset=0):
+        """adaLN + int8 quantization -> one QKV GEMM whose epilogue applies QK-norm (+RoPE) and writes q, k, v
+        head-major: out [3, B, H, L_total, D] (tokens at l_offset ..).  x [B, L, D]."""
+        b, n, d = x.shape
+        qa, sa = kernels.adaln_quant(x, shift1, scale1, group=self.group)
+        return kernels.qkv_heads(qa, sa, self.qkv.qw, self.qkv.sw, self.qkv.bias, self.q_norm_w, self.k_norm_w, b,
+                                 rope, out=out, l_offset=l_offset)
+
     def post(self, x, attn, gate1, shift2, scale2, gate2):
         """Out-projection + gated residual, then the MLP half with its gated residual.  attn [B, L, D]."""
         x = fused.gated_residual(x, kernels.block_linear(attn, self.proj.qw, self.proj.sw, self.proj.bias), gate1)
@@ -120,8 +128,8 @@ class DiTBlockInt8:
     def forward(self, x, mods, rope=None):
         """Self-attention over this stream only (torch SDPA, unchanged), then `post`."""
         shift1, scale1, gate1, shift2, scale2, gate2 = mods
-        q, k, v = self.attention_inputs(x, shift1, scale1, rope)
-        attn = attention(q, k, v).reshape(x.shape)
+        hm = self.attention_heads(x, shift1, scale1, rope)
+        attn = attention_heads(hm[0], hm[1], hm[2]).reshape(x.shape)
         return self.post(x, attn, gate1, shift2, scale2, gate2)
 
 
@@ -134,6 +142,16 @@ def attention(q, k, v):
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        out = F.scaled_dot_product_attention(qh, kh, vh)
+    return out.transpose(1, 2)
+
+
+def attention_heads(qh, kh, vh):
+    """`attention` on head-major operands qh, kh, vh [B, H, L, D] (contiguous, as the QKV epilogue writes
+    them): no layout copies before SDPA.  Returns [B, L, H, D] (a view of SDPA's output)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
     with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
         out = F.scaled_dot_product_attention(qh, kh, vh)
     return out.transpose(1, 2)
@@ -152,15 +170,15 @@ class DoubleStreamBlockInt8:
     def forward(self, img, txt, img_mods, txt_mods, rope=None):
         shift1, scale1, gate1, shift2, scale2, gate2 = img_mods
         tshift1, tscale1, tgate1, tshift2, tscale2, tgate2 = txt_mods
-        iq, ik, iv = self.img.attention_inputs(img, shift1, scale1, rope)
-        tq, tk, tv = self.txt.attention_inputs(txt, tshift1, tscale1, None)
-        q = torch.cat([iq, tq], dim=1)
-        k = torch.cat([ik, tk], dim=1)
-        v = torch.cat([iv, tv], dim=1)
-        del iq, ik, iv, tq, tk, tv
-        attn = attention(q, k, v)
-        del q, k, v
         b, lv = img.shape[0], img.shape[1]
+        # both streams' q, k, v land head-major in one buffer, image tokens first (the reference's
+        # torch.cat order), so attention runs on it without concatenation or layout copies
+        hm = torch.empty((3, b, self.img.heads, lv + txt.shape[1], img.shape[2] // self.img.heads),
+                         device=img.device, dtype=torch.bfloat16)
+        self.img.attention_heads(img, shift1, scale1, rope, out=hm, l_offset=0)
+        self.txt.attention_heads(txt, tshift1, tscale1, None, out=hm, l_offset=lv)
+        attn = attention_heads(hm[0], hm[1], hm[2])
+        del hm
         attn = attn.reshape(b, attn.shape[1], -1)
         img = self.img.post(img, attn[:, :lv], gate1, shift2, scale2, gate2)
         txt = self.txt.post(txt, attn[:, lv:], tgate1, tshift2, tscale2, tgate2)

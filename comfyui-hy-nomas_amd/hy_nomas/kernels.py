@@ -110,6 +110,56 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
     return (out, qs) if quantized else out
 
 
+def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="int8", eps=1e-6, out=None,
+              l_offset=0):
+    """The q/k/v projection with QK RMSNorm and RoPE in the GEMM epilogue, written head-major for attention
+    (hy_nomas/model.py:253-267 with fused.py:65-105): qa [batch * L, K] codes (scales sa), qw [3 * hidden, K]
+    the stacked q, k, v weights (scales sw, bias [3 * hidden] or None), norm weights [128], rope (cos, sin)
+    [L, 128] or None.  Returns `out` bf16 [3, batch, hidden / 128, L_total, 128] (allocated with
+    L_total = L when not given); tokens land at rows l_offset .. l_offset + L, so the image and text streams
+    can share one buffer.  q = out[0], k = out[1], v = out[2] are contiguous [B, H, L_total, 128]."""
+    _lib.require_device(qa, sa, qw, sw, bias, q_norm_w, k_norm_w)
+    m, k = qa.shape
+    n = qw.shape[0]
+    if n % 3 or (n // 3) % 128:
+        raise RuntimeError(f"qkv_heads: {n} weight rows are not q, k, v of whole 128-channel heads")
+    hidden = n // 3
+    if batch <= 0 or m % batch:
+        raise RuntimeError(f"qkv_heads: {m} token rows do not split into batch {batch}")
+    length = m // batch
+    if out is None:
+        out = torch.empty((3, batch, hidden // 128, length, 128), device=qa.device, dtype=torch.bfloat16)
+    if (out.dtype != torch.bfloat16 or out.dim() != 5 or tuple(out.shape[:3]) != (3, batch, hidden // 128)
+            or out.shape[4] != 128 or not out.is_contiguous() or out.shape[3] < l_offset + length):
+        raise RuntimeError(f"qkv_heads: out must be contiguous bf16 [3, {batch}, {hidden // 128}, >= {l_offset + length}, 128]")
+    if m == 0:
+        return out
+    sw_rows = 1 if sw.shape[0] == n else GROUP
+    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1:
+        group, groups = k, 1
+    else:
+        group, groups = GROUP, k // GROUP
+    sa = _scales(sa, m, groups)
+    sw = _scales(sw, sw.shape[0], groups)
+    qa, qw = _rows(qa), _rows(qw)
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    wq = q_norm_w.to(torch.bfloat16).float().contiguous()
+    wk = k_norm_w.to(torch.bfloat16).float().contiguous()
+    if rope is not None:
+        cos, sin = rope[0].float().contiguous(), rope[1].float().contiguous()
+        if tuple(cos.shape) != (length, 128) or tuple(sin.shape) != (length, 128):
+            raise RuntimeError(f"rope tables must be [L, 128] = {(length, 128)}, got {tuple(cos.shape)}")
+        cp, sp = cos.data_ptr(), sin.data_ptr()
+    else:
+        cp = sp = None
+    _lib.call("hn_qkv_heads", qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
+              sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
+              batch, length, hidden, k, group, _lib.KIND[kind], wq.data_ptr(), wk.data_ptr(), cp, sp, eps,
+              out.data_ptr(), out.shape[3], l_offset, _lib.stream(qa))
+    return out
+
+
 def block_gemm_acc32(qa, qw):
     """Full-K int32 dot products qa @ qw^T of int8 codes (a test hook: the exact integer accumulator)."""
     _lib.require_device(qa, qw)

@@ -93,6 +93,26 @@ int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, co
                   int64_t ldqs, void* stream);
 
 /*
+ * The QKV projection of a double-stream block with QK-norm and RoPE in its epilogue, written head-major
+ * for attention.  Replaces the block_gemm of the three q/k/v linears plus the two fused.qk_norm_rope
+ * calls of DoubleStreamBlock._qkv (hy_nomas/model.py:253-267, fused.py:65-105), and the [B, L, H, D] ->
+ * [B, H, L, D] copies attention makes of q, k and v.
+ *   qa [B * L, K] codes with scales sa, qw [3 * hidden, K] = the q, k and v weights stacked (scales sw
+ *   [3 * hidden / sw_rows, K / group], bias [3 * hidden] or NULL), as hn_block_gemm;
+ *   out bf16 [3, B, hidden / 128, L_total, 128]: part 0/1/2 = q/k/v, token l of batch b at row
+ *   l_offset + l, so two streams (image, text) can fill one buffer at their own token offsets.
+ * q and k: x = bf16(projection), r = 1 / sqrt(mean over the head's 128 channels of x^2 + eps),
+ * n = bf16(bf16(x r) * w) with w = q_norm_w / k_norm_w ([128] fp32), then, if cos/sin ([L, 128] fp32) are
+ * given, (n_2i c_2i - n_2i+1 s_2i, n_2i+1 c_2i+1 + n_2i s_2i+1) for the pairs (2i, 2i + 1).  v: bf16.
+ * Head dim 128; hidden % 128 == 0.
+ */
+int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                 const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
+                 int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
+                 const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
+                 int64_t L_total, int64_t l_offset, void* stream);
+
+/*
  * LayerNorm (or RMSNorm) + adaLN modulate.  Replaces fused.adaln / _adaln_kernel (hy_nomas/fused.py:37-62).
  *   x [B, L, D] contiguous (x_dtype bf16 or fp16), shift/scale [B, D] -> y [B, L, D] (same dtype):
  *   y = norm(x) * bf16(1 + scale[b]) + shift[b].
