@@ -21,7 +21,10 @@ static int cu_count() {
   return cached[dev];
 }
 
-template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK = false>
+// WPE: waves per SIMD the kernel is compiled for; above WN * WM / 4, several workgroups share a CU and the
+// persistent grid grows to match.
+template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK = false,
+          int WPE = WN * WM / 4>
 static int launch_cfg(GemmArgs& a, hipStream_t st) {
   constexpr int BN = WN * TN * 32, BM = WM * TM * 32;
   const int64_t tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
@@ -31,28 +34,32 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
   }
   a.tiles_m = (int)tm;
   a.tiles_n = (int)tn;
-  const int64_t grid = tm * tn < cu_count() ? tm * tn : cu_count();
-  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS, WBLK>), dim3((unsigned)grid),
-                     dim3(WN * WM * 64), 0, st, a);
+  const int64_t slots = (int64_t)cu_count() * (WPE * 4 / (WN * WM));
+  const int64_t grid = tm * tn < slots ? tm * tn : slots;
+  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS, WBLK, false, WPE>),
+                     dim3((unsigned)grid), dim3(WN * WM * 64), 0, st, a);
   return HN_LAUNCH_CHECK("block_gemm_kernel");
 }
 
-// per-token / per-channel: 256 x 256 tile, 8 waves of 128 x 64.  g128: 256 x 128, 8 waves of 128 x 32.
-// 128-byte K stages in two LDS buffers.
+// per-token / per-channel: 256 x 256 tile, 8 waves of 128 x 64.  fp8 with block weight scales: the same
+// tile (the running sum is rescaled in place, so there is no second accumulator set).  Other g128 layouts:
+// 128 x 128 tiles of 4 waves of 128 x 32, two workgroups per CU.  128-byte K stages in two LDS buffers.
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
-  // fp8 with block weight scales rescales its running sum in place (no second accumulator set), so it
-  // fits the 256 x 256 tile
-  // swiglu_quant splits each wave's tokens between the gate and up waves, so it needs two token blocks
-  // per wave (TM = 2): the per-token tile, or fp8 with block weight scales
   constexpr bool SWIGLU = EPI == HN_EPI_SWIGLU_QUANT;
-  if (g128 && a.sw_rows == 128) {
-    if constexpr (!SWIGLU || KIND == HN_KIND_FP8)
-      return launch_cfg<KIND, EPI, true, 2, 4, 4, KIND == HN_KIND_FP8 ? 2 : 1, OUT_DT, 128, 2, true>(a, st);
-  } else if (g128) {
-    if constexpr (!SWIGLU) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
-  } else {
-    return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+  if (!g128) return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+  if constexpr (KIND == HN_KIND_FP8) {
+    if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2, true>(a, st);
+  }
+  // The g128 fold (three VALU ops per output and group) bounds these layouts.  With two independent
+  // workgroups per CU one can fold while the other keeps the matrix cores busy, which the per-stage
+  // barrier of a single 8-wave workgroup prevents (DiT stack: int8 1.13x, fp8 with expanded block
+  // scales 1.16x over one 256 x 128 workgroup per CU).
+  if constexpr (!SWIGLU) {
+    if constexpr (KIND == HN_KIND_INT8) {  // (fp8 block scales took the branch above)
+      if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 1, 4, 4, 1, OUT_DT, 128, 2, true, 2>(a, st);
+    }
+    return launch_cfg<KIND, EPI, true, 1, 4, 4, 1, OUT_DT, 128, 2, false, 2>(a, st);
   }
   set_error("hn_block_gemm: swiglu_quant needs per-token scales or fp8 with 128 x 128 block weight scales");
   return HN_ERR_UNSUPPORTED;

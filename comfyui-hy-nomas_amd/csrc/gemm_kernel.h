@@ -196,8 +196,8 @@ __device__ __forceinline__ uint32_t cvt2_out(float a, float b) {
 // The first stage of the next tile is issued before the current tile's epilogue, so its load latency
 // hides behind the epilogue and the epilogue's stores drain while it lands.
 template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK,
-          bool AV = false>
-__global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WN * WM / 4, WN * WM / 4)))
+          bool AV = false, int WPE = WN * WM / 4>
+__global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void block_gemm_kernel(const GemmArgs a) {
   using MF = Mfma<KIND>;
   using Acc = typename MF::Acc;
