@@ -28,6 +28,8 @@ def adaln(x, shift, scale, eps=1e-6, norm="layer"):
     (hy_nomas/fused.py:55-62).  `norm="rms"` uses RMSNorm."""
     _lib.require_device(x, shift, scale)
     b, l, d = x.shape
+    if shift.numel() != b * d or scale.numel() != b * d:
+        raise RuntimeError(f"adaln: shift/scale must be [B, D] = {(b, d)}")
     x = x.contiguous()
     y = torch.empty(x.shape, device=x.device, dtype=x.dtype)
     if b * l == 0:
@@ -45,6 +47,8 @@ def qk_norm_rope(x, weight, rope=None, eps=1e-6):
     (hy_nomas/fused.py:94-105)."""
     _lib.require_device(x, weight)
     b, l, h, d = x.shape
+    if weight.numel() != d:
+        raise RuntimeError(f"qk_norm_rope: weight must have the head dim's {d} values")
     if x.stride(3) != 1 or x.stride(2) != d or x.stride(0) != l * x.stride(1) or x.data_ptr() % 16 \
             or x.stride(1) % 8:
         x = x.contiguous()
@@ -69,6 +73,8 @@ def gated_residual(x, y, gate):
     (hy_nomas/fused.py:121-128)."""
     _lib.require_device(x, y, gate)
     b, l, d = x.shape
+    if tuple(y.shape) != (b, l, d) or gate.numel() != b * d:
+        raise RuntimeError(f"gated_residual: y must be [B, L, D] = {(b, l, d)} and gate [B, D]")
     x = x.contiguous()
     y = y.contiguous()
     gate = gate.to(x.dtype).contiguous()
@@ -87,6 +93,8 @@ def gated_residual_frames(x, y, gate, frame):
     with the same two roundings."""
     _lib.require_device(x, y, gate, frame)
     b, l, d = x.shape
+    if tuple(y.shape) != (b, l, d) or gate.numel() != b * d or frame.dim() != 3:
+        raise RuntimeError(f"gated_residual_frames: y must be [B, L, D] = {(b, l, d)}, gate [B, D], frame 3-D")
     t = frame.shape[1]
     if frame.shape[0] not in (1, b) or frame.shape[2] != d or t == 0 or l % t:
         raise RuntimeError(f"gated_residual_frames: frame {tuple(frame.shape)} does not tile x {tuple(x.shape)}")

@@ -48,6 +48,31 @@ def quantize_activations(x, kind="int8", group=GROUP, rounding="half_away"):
     return q, s
 
 
+_CODE_DTYPES = {"int8": (torch.int8,), "fp8": (torch.float8_e4m3fn, torch.uint8)}
+
+
+def _check_gemm(qa, sa, qw, sw, bias, kind):
+    """Shapes and dtypes the kernels rely on (the C ABI sees only pointers and strides): codes of the kind,
+    matching K, one activation-scale row per token, weight-scale rows for every output channel (one per
+    channel or one per 128), a bias of N values.  Raises RuntimeError."""
+    if kind not in _CODE_DTYPES:
+        raise RuntimeError(f"kind must be 'int8' or 'fp8', got {kind!r}")
+    if qa.dim() != 2 or qw.dim() != 2 or sa.dim() != 2 or sw.dim() != 2:
+        raise RuntimeError("block_gemm: codes and scales must be 2-D")
+    if qa.dtype not in _CODE_DTYPES[kind] or qw.dtype not in _CODE_DTYPES[kind]:
+        raise RuntimeError(f"block_gemm: {kind} codes expected, got {qa.dtype} / {qw.dtype}")
+    m, k = qa.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k:
+        raise RuntimeError(f"block_gemm: activations have K={k}, weights K={qw.shape[1]}")
+    if sa.shape[0] != m:
+        raise RuntimeError(f"block_gemm: {sa.shape[0]} activation-scale rows for {m} tokens")
+    if sw.shape[0] not in (n, (n + GROUP - 1) // GROUP):
+        raise RuntimeError(f"block_gemm: {sw.shape[0]} weight-scale rows for {n} output channels")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != n):
+        raise RuntimeError(f"block_gemm: bias of shape {tuple(bias.shape)} for {n} output channels")
+
+
 def _scales(s, rows, groups):
     """fp32 [rows, groups] with unit column stride; a single column is broadcast to `groups` columns."""
     s = s.float()
@@ -71,6 +96,7 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
     bf16(silu(gate) * up) in this GEMM's kind, [M, N / 2], and their scales [M, N / 256], ready for the
     down projection.  Needs per-token scales, or fp8 with block weight scales."""
     _lib.require_device(qa, sa, qw, sw, bias)
+    _check_gemm(qa, sa, qw, sw, bias, kind)
     m, k = qa.shape
     n = qw.shape[0]
     mode = EPILOGUES[epilogue]
@@ -119,6 +145,9 @@ def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="
     L_total = L when not given); tokens land at rows l_offset .. l_offset + L, so the image and text streams
     can share one buffer.  q = out[0], k = out[1], v = out[2] are contiguous [B, H, L_total, 128]."""
     _lib.require_device(qa, sa, qw, sw, bias, q_norm_w, k_norm_w)
+    _check_gemm(qa, sa, qw, sw, bias, kind)
+    if q_norm_w.numel() != 128 or k_norm_w.numel() != 128:
+        raise RuntimeError("qkv_heads: QK-norm weights must have the head dim's 128 values")
     m, k = qa.shape
     n = qw.shape[0]
     if n % 3 or (n // 3) % 128:
@@ -165,6 +194,8 @@ def block_gemm_acc32(qa, qw):
     _lib.require_device(qa, qw)
     m, k = qa.shape
     n = qw.shape[0]
+    if qa.dtype != torch.int8 or qw.dtype != torch.int8 or qw.shape[1] != k:
+        raise RuntimeError("block_gemm_acc32: int8 codes with matching K expected")
     out = torch.empty((m, n), device=qa.device, dtype=torch.int32)
     if m == 0:
         return out
@@ -183,6 +214,8 @@ def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away", g
     D <= 4096)."""
     _lib.require_device(x, shift, scale)
     b, l, d = x.shape
+    if shift.numel() != b * d or scale.numel() != b * d:
+        raise RuntimeError(f"adaln_quant: shift/scale must be [B, D] = {(b, d)}")
     g = d if group is None else group
     x = x.contiguous()
     shift = shift.to(x.dtype).contiguous()

@@ -289,3 +289,33 @@ def test_modulation_linear_from_silu_vec(dev):
     ref = torch.nn.functional.linear(x.float().cpu(), ops.dequantize_g128(q, s, torch.float32), bias.float())
     assert got.shape == (1, 18432)
     assert ((got.float().cpu() - ref).norm() / ref.norm()).item() < 2e-2
+
+
+def test_wrappers_reject_mismatched_operands(dev):
+    """The C ABI sees pointers and strides only; the Python wrappers refuse operands whose shapes or dtypes
+    would make a kernel read past a tensor (K mismatch, short scale or bias tensors, wrong code type)."""
+    from hy_nomas import fused, kernels
+
+    print("wrapper validation", flush=True)
+    g = seeded(31)
+    x = torch.randn(64, 256, generator=g).to(torch.bfloat16).to(dev)
+    qa, sa = kernels.quantize_activations(x)
+    w = torch.randint(-127, 128, (128, 256), generator=g, dtype=torch.int8).to(dev)
+    sw = (torch.rand(128, 2, generator=g) * 1e-3 + 1e-3).to(dev)
+    kernels.block_gemm(qa, sa, w, sw)                                  # the valid call
+    bad = [
+        lambda: kernels.block_gemm(qa, sa, w[:, :128].contiguous(), sw[:, :1].contiguous()),  # K mismatch
+        lambda: kernels.block_gemm(qa, sa[:63], w, sw),                                       # short sa
+        lambda: kernels.block_gemm(qa, sa, w, sw[:100]),                                      # short sw
+        lambda: kernels.block_gemm(qa, sa, w, sw, torch.zeros(100, device=dev)),              # short bias
+        lambda: kernels.block_gemm(qa, sa, w, sw, kind="fp8"),                                # int8 codes as fp8
+        lambda: kernels.block_gemm_acc32(qa, w[:, :128].contiguous()),
+        lambda: kernels.adaln_quant(x.view(1, 64, 256), torch.zeros(1, 128, device=dev), torch.zeros(1, 256, device=dev)),
+        lambda: fused.adaln(x.view(1, 64, 256), torch.zeros(1, 256, device=dev), torch.zeros(1, 200, device=dev)),
+        lambda: fused.gated_residual(x.view(1, 64, 256), x.view(1, 64, 256)[:, :32], torch.zeros(1, 256, device=dev)),
+        lambda: fused.qk_norm_rope(x.view(1, 64, 2, 128), torch.ones(64, device=dev)),
+    ]
+    for i, fn in enumerate(bad):
+        with pytest.raises(RuntimeError):
+            fn()
+        print(f"  rejected case {i}", flush=True)
