@@ -32,6 +32,7 @@
 #pragma once
 
 #include <type_traits>
+#include <utility>
 
 #include "hn_common.h"
 
@@ -152,6 +153,20 @@ struct Mfma<HN_KIND_FP8> {
   __device__ __forceinline__ static float get(const Acc& c, int r) { return c[r]; }
   __device__ __forceinline__ static void put(Acc& c, int r, float v) { c[r] = v; }
 };
+
+// facc[r] = fma(float(part[r]) * sa, w, facc[r]) where w is lane (l & ~15) + r of `w16` (a DPP row
+// broadcast of lane r of the caller's 16-lane row): one v_fmac_f32_dpp per output.  The fma is the
+// same single rounding as __builtin_fmaf.
+template <int R>
+__device__ __forceinline__ float fmac_row_bcast(float acc, float w16, float t) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(w16), "v"(t), "n"(R));
+  return acc;
+}
+template <typename Acc, int... R>
+__device__ __forceinline__ void fold_row_bcast(v16f& facc, const Acc& part, float sa, float w16,
+                                               std::integer_sequence<int, R...>) {
+  ((facc[R] = fmac_row_bcast<R>(facc[R], w16, (float)part[R] * sa)), ...);
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -528,26 +543,29 @@ void block_gemm_kernel(const GemmArgs a) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
           const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
           const float swb = WBLK ? sc[wn * TN * 32] : 0.0f;  // the wave's one weight scale (block layout)
+          // Per-channel scales: lane l needs the scale of channel 32 i + 8 rr + 4 (l >> 5) + q for each
+          // (i, rr, q), the same for the 32 lanes of a half-wave.  Lane (row R = l >> 4, s = l & 15) loads
+          // the one of channel 32 i + 8 (s >> 2) + 4 (R >> 1) + (s & 3), and the fma reads it with a DPP
+          // row broadcast of lane s = 4 rr + q (one LDS read per lane per i instead of 16 bytes per output
+          // quad).
+          float swc[WBLK ? 1 : TN];
+          if constexpr (!WBLK) {
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+              swc[i] = sc[wn * TN * 32 + i * 32 + ((lane & 15) >> 2) * 8 + (lane >> 5) * 4 + (lane & 3)];
+          }
 #pragma unroll
           for (int j = 0; j < TM; j++) {
             const float sam = sc[BN + wrow_m + j * 32];
             const float ss = sam * swb;
 #pragma unroll
             for (int i = 0; i < TN; i++) {
+              if constexpr (WBLK) {
 #pragma unroll
-              for (int rr = 0; rr < 4; rr++) {
-                if constexpr (WBLK) {
-#pragma unroll
-                  for (int qq = 0; qq < 4; qq++)
-                    facc[i][j][rr * 4 + qq] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + qq]), ss, facc[i][j][rr * 4 + qq]);
-                } else {
-                  const float4 swv =
-                      *reinterpret_cast<const float4*>(sc + wn * TN * 32 + i * 32 + rr * 8 + (lane >> 5) * 4);
-                  facc[i][j][rr * 4 + 0] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 0]) * sam, swv.x, facc[i][j][rr * 4 + 0]);
-                  facc[i][j][rr * 4 + 1] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 1]) * sam, swv.y, facc[i][j][rr * 4 + 1]);
-                  facc[i][j][rr * 4 + 2] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 2]) * sam, swv.z, facc[i][j][rr * 4 + 2]);
-                  facc[i][j][rr * 4 + 3] = __builtin_fmaf(MF::to_f32(acc[i][j][rr * 4 + 3]) * sam, swv.w, facc[i][j][rr * 4 + 3]);
-                }
+                for (int r = 0; r < 16; r++)
+                  facc[i][j][r] = __builtin_fmaf(MF::to_f32(acc[i][j][r]), ss, facc[i][j][r]);
+              } else {
+                fold_row_bcast(facc[i][j], acc[i][j], sam, swc[i], std::make_integer_sequence<int, 16>());
               }
             }
           }
