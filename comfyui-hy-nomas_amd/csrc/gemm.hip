@@ -43,7 +43,8 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
 
 // per-token / per-channel: 256 x 256 tile, 8 waves of 128 x 64.  fp8 with block weight scales: the same
 // tile (the running sum is rescaled in place, so there is no second accumulator set).  Other g128 layouts:
-// 128 x 128 tiles of 4 waves of 128 x 32, two workgroups per CU.  128-byte K stages in two LDS buffers.
+// 256 x 128, 8 waves of 128 x 32 (the int32 group partial and the fp32 running sum both fit in 256
+// VGPRs).  128-byte K stages in two LDS buffers.
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
   constexpr bool SWIGLU = EPI == HN_EPI_SWIGLU_QUANT;
@@ -51,15 +52,11 @@ static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
   if constexpr (KIND == HN_KIND_FP8) {
     if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2, true>(a, st);
   }
-  // The g128 fold (three VALU ops per output and group) bounds these layouts.  With two independent
-  // workgroups per CU one can fold while the other keeps the matrix cores busy, which the per-stage
-  // barrier of a single 8-wave workgroup prevents (DiT stack: int8 1.13x, fp8 with expanded block
-  // scales 1.16x over one 256 x 128 workgroup per CU).
   if constexpr (!SWIGLU) {
     if constexpr (KIND == HN_KIND_INT8) {  // (fp8 block scales took the branch above)
-      if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 1, 4, 4, 1, OUT_DT, 128, 2, true, 2>(a, st);
+      if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2, true>(a, st);
     }
-    return launch_cfg<KIND, EPI, true, 1, 4, 4, 1, OUT_DT, 128, 2, false, 2>(a, st);
+    return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
   }
   set_error("hn_block_gemm: swiglu_quant needs per-token scales or fp8 with 128 x 128 block weight scales");
   return HN_ERR_UNSUPPORTED;
