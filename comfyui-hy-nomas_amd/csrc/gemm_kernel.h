@@ -101,9 +101,14 @@ __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // kernels.py:74-77, fp32, evaluated in the order written
-  float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  float sig = 1.0f / (1.0f + expf(-(2.0f * inner)));
+  // kernels.py:74-77 in fp32, in the order written, with sigmoid(2 inner) = 1 / (1 + exp(-2 inner)) taken
+  // from the hardware base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each).  The
+  // result carries a few fp32 ulps of error, which the bf16 rounding that follows hides for all but
+  // about 1e-4 of the outputs (the reference's tolerance is 1e-3).  exp overflowing to inf gives
+  // sigmoid 0, and underflowing to 0 gives 1, as the exact function.
+  const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float e = __builtin_amdgcn_exp2f(inner * -2.8853900817779268f);  // exp(-2 inner)
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
   return 0.5f * x * (1.0f + (2.0f * sig - 1.0f));
 }
 

@@ -1,7 +1,7 @@
 """Block-scaled int8 / fp8 GEMM on the GPU vs the CPU oracle (hy_nomas/kernels.py:80-170).
 
 int8: the int32 accumulators are exact and the fp32 epilogue runs the oracle's operation sequence, so the
-outputs must match the oracle bit for bit.  gelu uses the device expf, so its bf16 outputs may differ
+outputs must match the oracle bit for bit.  gelu uses the hardware exp2 and reciprocal, so its bf16 outputs may differ
 in rare last-bit cases (the reference test's tolerances apply).  fp8: fp32 accumulation inside the
 matrix core has its own order; checked to 1e-2 max-abs-rel against the fp64 product of the dequantized
 operands (and tightly against the oracle)."""
