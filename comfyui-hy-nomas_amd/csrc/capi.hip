@@ -23,6 +23,6 @@ int hip_status(hipError_t e, const char* what) {
 
 }  // namespace hn
 
-extern "C" int hn_version(void) { return 100; }
+extern "C" int hn_version(void) { return 200; }
 
 extern "C" const char* hn_last_error(void) { return hn::g_error; }

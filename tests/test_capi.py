@@ -67,3 +67,11 @@ def test_argument_validation_without_a_gpu():
     rc = l.hn_block_gemm(None, 256, None, 2, None, 256, None, 2, 128, None, 0, 4, 512, 256, 128, 1, 4, None, 0, 256,
                          None, 1, None)   # swiglu_quant scales [M, N/256] missing
     assert rc == 1 and b"swiglu_quant" in l.hn_last_error()
+    rc = l.hn_qkv_heads(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 1, 64, 200, 256, 128, 0, None, None,
+                        None, None, 1e-6, None, 64, 0, None)   # hidden 200: not whole 128-channel heads
+    assert rc == 1 and b"hidden" in l.hn_last_error()
+    rc = l.hn_qkv_heads(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 1, 64, 256, 256, 128, 0, None, None,
+                        None, None, 1e-6, None, 70, 10, None)  # tokens [10, 74) past L_total 70
+    assert rc == 1 and b"L_total" in l.hn_last_error()
+    rc = l.hn_gated_residual_frames(None, None, None, None, 0, 1, 2, 3, 100, None, None)   # D % 8 != 0
+    assert rc == 1 and b"multiple of 8" in l.hn_last_error()
