@@ -36,7 +36,9 @@ HIDDEN = 3072
 # Memory-side bytes per headline step (4 GEMM launches) from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
 # script, scaled by a plain-copy calibration (FETCH x2.0, WRITE x1.0); profiles/block_gemm_int8_per_token_M32768.md
 TRAFFIC_BYTES_PER_STEP = 7.26e9
-SLEEP_CYCLES = 2e8           # ~0.1 s of spin before each timed region
+SLEEP_CYCLES = 2e8           # ~80 ms of spin before each timed region
+HOT_S = 0.1                  # seconds of untimed passes between the spin and the timed region
+HOT_MAX_LAUNCHES = 2000
 WARM_S = 1.5                 # seconds of untimed GEMM work before the headline's timed region
 STACK = [("qkv", 3072, 9216), ("attn_out", 3072, 3072), ("ffn_up", 3072, 12288), ("ffn_down", 12288, 3072)]
 
@@ -66,33 +68,57 @@ def time_launches(fns, steps, warmup, warm_s=0.0):
     pair around all steps, the per-launch averages from a second pass with an event pair around every launch.
     Before the timed region: `warmup` untimed passes, then more untimed passes until `warm_s` seconds have
     elapsed, so the GPU clocks reach the steady state of this work (they take about a second to settle under
-    a matrix-core load)."""
+    a matrix-core load).
+
+    Each timed pass is queued behind a spin kernel, so the events measure GPU time and not the host's
+    per-call overhead (which exceeds a 50 us elementwise kernel).  The spin leaves the chip nearly idle for
+    ~80 ms, and the first ~30 ms of matrix-core work after such an idle period run up to 25 % slower than
+    the sustained rate while the power controller settles; so HOT_S seconds of untimed passes sit between
+    the spin and the start event."""
     for _ in range(warmup):
         for f in fns:
             f()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < warm_s:
+    passes = 0
+    while passes == 0 or time.perf_counter() - t0 < warm_s:
         for f in fns:
             f()
         torch.cuda.synchronize()
+        passes += 1
+    pass_s = (time.perf_counter() - t0) / passes
+    hot = max(1, min(int(HOT_S / pass_s) + 1, HOT_MAX_LAUNCHES // len(fns)))
     stream = torch.cuda.current_stream()
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in fns]
           for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    # a spin kernel holds the GPU while the host queues every timed launch, so the events measure GPU time
-    # and not the host's per-call overhead (which exceeds a 50 us elementwise kernel)
-    torch.cuda._sleep(int(SLEEP_CYCLES))
+    spin0 = torch.cuda.Event(enable_timing=True)
+
+    def spin_then_hot():
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        spin0.record(stream)
+        torch.cuda._sleep(int(SLEEP_CYCLES))
+        for _ in range(hot):
+            for f in fns:
+                f()
+        return t
+
+    t = spin_then_hot()
     start.record(stream)
     for s in range(steps):
         for f in fns:
             f()
     end.record(stream)
+    host_s = time.perf_counter() - t
     torch.cuda.synchronize()
+    ahead_ms = spin0.elapsed_time(start)
+    if host_s * 1e3 > ahead_ms:
+        log(f"bench: host queueing took {host_s * 1e3:.1f} ms, the GPU reached the timed region after "
+            f"{ahead_ms:.1f} ms: part of the timed region waited for the host")
     total_ms = start.elapsed_time(end) / steps
     # a second pass with an event pair around every launch, for the per-launch averages
-    torch.cuda._sleep(int(SLEEP_CYCLES))
+    spin_then_hot()
     for s in range(steps):
         for i, f in enumerate(fns):
             ev[s][i][0].record(stream)
