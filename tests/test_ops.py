@@ -1,0 +1,143 @@
+"""The Linear op family that loads Tencent's int8 g128 weights and picks the matmul (hy_nomas/ops.py:104-191):
+state-dict loading and its errors, the exact path against the dequantized weight, the matmul-mode switches
+(`with_matmul`, HY_NOMAS_MATMUL), re-quantization on `set_weight`, `fast_int8` / `int8_weights`, and on the
+GPU the int8 matrix-core path against block_linear and against the exact path."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import seeded
+
+
+def tencent_pair(n, k, seed):
+    """A `weight_q` / `weight_scale` pair as the reference's checkpoints hold it (ops.py:41-52 on a bf16 weight)."""
+    w = (torch.randn(n, k, generator=seeded(seed)) * 0.02).to(torch.bfloat16)
+    q, s = oracle.quantize_g128(w)
+    return torch.from_numpy(q), torch.from_numpy(s)
+
+
+def make_linear(ops_cls, n, k, seed, bias=True, dtype=torch.bfloat16):
+    from hy_nomas import ops
+
+    lin = ops_cls.Linear(k, n, bias=bias, dtype=dtype)
+    q, s = tencent_pair(n, k, seed)
+    sd = {"weight_q": q, "weight_scale": s}
+    b = (torch.randn(n, generator=seeded(seed + 1)) * 0.02).to(torch.bfloat16)
+    if bias:
+        sd["bias"] = b
+    missing, errors = [], []
+    lin._load_from_state_dict(sd, "", {}, True, missing, [], errors)
+    assert not missing and not errors
+    assert ops.is_quantized(lin.weight)
+    return lin, q, s, b
+
+
+def test_load_and_exact_forward_is_dequantize_then_linear():
+    from hy_nomas import ops
+
+    n, k = 96, 300  # K not a multiple of 128: the last group is partial
+    lin, q, s, b = make_linear(ops.NomasOps, n, k, seed=3)
+    assert torch.equal(lin.weight._qdata, q) and torch.equal(lin.weight._params.scale, s)
+    x = torch.randn(2, 5, k, generator=seeded(4)).to(torch.bfloat16)
+    got = lin(x)
+    w = torch.from_numpy(oracle.dequantize_g128(q.numpy(), s.numpy())).to(torch.bfloat16)
+    assert torch.equal(got, torch.nn.functional.linear(x, w, b))
+    assert got.shape == (2, 5, n) and got.dtype == torch.bfloat16
+
+
+def test_load_errors_and_plain_weights():
+    from hy_nomas import ops
+
+    q, s = tencent_pair(64, 128, seed=5)
+    lin = ops.NomasOps.Linear(128, 64, bias=True)
+    missing, errors = [], []
+    lin._load_from_state_dict({"blk.weight_q": q}, "blk.", {}, True, missing, [], errors)
+    assert errors == ["blk.weight_q without blk.weight_scale"] and lin.weight is None
+    errors.clear()
+    lin._load_from_state_dict({"blk.weight_q": q[:, :64], "blk.weight_scale": s}, "blk.", {}, True, missing, [],
+                             errors)
+    assert len(errors) == 1 and "expected (64, 128)" in errors[0]
+    errors.clear()
+    lin._load_from_state_dict({}, "blk.", {}, True, missing, [], errors)
+    assert missing == ["blk.weight"]
+    missing.clear()
+    # a plain weight stays a plain parameter, cast to the layer dtype; a missing bias is reported
+    lin = ops.NomasOps.Linear(128, 64, bias=True, dtype=torch.bfloat16)
+    plain = torch.randn(64, 128, generator=seeded(6))
+    lin._load_from_state_dict({"blk.weight": plain}, "blk.", {}, True, missing, [], errors)
+    assert missing == ["blk.bias"] and not errors
+    assert not ops.is_quantized(lin.weight) and lin.weight.dtype == torch.bfloat16
+    assert ops.quantized_linears(torch.nn.Sequential(lin)) == []
+
+
+def test_matmul_mode_switches(monkeypatch):
+    from hy_nomas import ops
+
+    int8_ops = ops.NomasOps.with_matmul("int8")
+    assert int8_ops.Linear.default_matmul == "int8" and ops.NomasOps.Linear.default_matmul == "exact"
+    assert issubclass(int8_ops.Linear, ops.NomasOps.Linear)
+    lin, _, _, _ = make_linear(int8_ops, 64, 256, seed=7)
+    x = torch.randn(3, 256, generator=seeded(8)).to(torch.bfloat16)
+    # CPU input: never the int8 path, whatever the mode
+    assert not lin.fast_int8(x)
+    exact, _, _, _ = make_linear(ops.NomasOps, 64, 256, seed=7)
+    assert torch.equal(lin(x), exact(x))
+    monkeypatch.setenv(ops.MATMUL_ENV, "int8")
+    assert ops.matmul_mode() == "int8"
+    monkeypatch.delenv(ops.MATMUL_ENV)
+    assert ops.matmul_mode() == "exact" and ops.matmul_mode("int8") == "int8"
+
+
+def test_set_weight_requantizes_and_int8_weights_yields_the_codes():
+    from hy_nomas import ops
+
+    lin, q, s, b = make_linear(ops.NomasOps, 64, 256, seed=9)
+    new = (torch.randn(64, 256, generator=seeded(10)) * 0.05).to(torch.bfloat16)
+    lin.set_weight(new)
+    q2, s2 = oracle.quantize_g128(new)
+    assert torch.equal(lin.weight._qdata, torch.from_numpy(q2))
+    assert np.array_equal(lin.weight._params.scale.numpy(), s2)
+    with lin.int8_weights(torch.zeros(1, 256, dtype=torch.bfloat16)) as (qd, sc, bias):
+        assert torch.equal(qd, torch.from_numpy(q2)) and torch.equal(bias, b)
+
+
+@pytest.mark.gpu
+def test_int8_mode_runs_the_matrix_core_path(dev):
+    """int8 mode on a device input: bit-identical to block_linear (per-token-and-group quantization + the
+    g128 GEMM), within the north-star 1e-2 of the exact path, and `fast_int8` holds."""
+    from hy_nomas import kernels, ops
+
+    print("ops.Linear int8 mode", flush=True)
+    lin, q, s, b = make_linear(ops.NomasOps.with_matmul("int8"), 384, 1024, seed=11)
+    lin = lin.to(dev)
+    x = (torch.randn(2, 77, 1024, generator=seeded(12)) * 2).to(torch.bfloat16).to(dev)
+    assert lin.fast_int8(x)
+    got = lin(x)
+    ref = kernels.block_linear(x, q.to(dev), s.to(dev), b.to(dev))
+    assert torch.equal(got, ref)
+    exact = ops.NomasOps.Linear(1024, 384, bias=True, dtype=torch.bfloat16)
+    exact._load_from_state_dict({"weight_q": q, "weight_scale": s, "bias": b}, "", {}, True, [], [], [])
+    want = exact.to(dev)(x).float()
+    assert ((got.float() - want).abs().max() / want.abs().max()).item() < 1e-2
+    with lin.int8_weights(x) as (qd, sc, bias):
+        assert qd.device == x.device and torch.equal(qd.cpu(), q)
+
+
+@pytest.mark.gpu
+def test_block_linear_takes_the_reference_fallback_for_empty_and_ragged_k(dev):
+    """M = 0 and K % 128 != 0 take the reference's dequantize + F.linear branch (kernels.py:216-218)."""
+    from hy_nomas import kernels
+
+    print("block_linear fallback shapes", flush=True)
+    q, s = tencent_pair(64, 256, seed=13)
+    out = kernels.block_linear(torch.empty(0, 256, dtype=torch.bfloat16, device=dev), q.to(dev), s.to(dev))
+    assert out.shape == (0, 64) and out.dtype == torch.bfloat16
+    q, s = tencent_pair(64, 200, seed=14)
+    x = torch.randn(2, 3, 200, generator=seeded(15)).to(torch.bfloat16)
+    b = (torch.randn(64, generator=seeded(16)) * 0.02).to(torch.bfloat16)
+    got = kernels.block_linear(x.to(dev), q.to(dev), s.to(dev), b.to(dev)).cpu()
+    w = torch.from_numpy(oracle.dequantize_g128(q.numpy(), s.numpy())).to(torch.bfloat16)
+    want = torch.nn.functional.linear(x.float(), w.float(), b.float())
+    assert got.shape == (2, 3, 64)
+    assert ((got.float() - want).abs().max() / want.abs().max()).item() < 1e-2
