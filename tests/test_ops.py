@@ -141,3 +141,23 @@ def test_block_linear_takes_the_reference_fallback_for_empty_and_ragged_k(dev):
     want = torch.nn.functional.linear(x.float(), w.float(), b.float())
     assert got.shape == (2, 3, 64)
     assert ((got.float() - want).abs().max() / want.abs().max()).item() < 1e-2
+
+
+def test_fused_gate(monkeypatch):
+    """fused.available: HY_NOMAS_FUSED != "0" at import, a device tensor, bf16 (fused.py:22-26)."""
+    import importlib
+
+    from hy_nomas import fused
+
+    assert fused.ENABLED
+    assert not fused.available(torch.zeros(2, dtype=torch.bfloat16))
+    monkeypatch.setenv("HY_NOMAS_FUSED", "0")
+    try:
+        assert not importlib.reload(fused).ENABLED
+    finally:
+        monkeypatch.delenv("HY_NOMAS_FUSED")
+        importlib.reload(fused)
+    assert fused.ENABLED
+    if torch.cuda.is_available():
+        assert fused.available(torch.zeros(2, dtype=torch.bfloat16, device="cuda"))
+        assert not fused.available(torch.zeros(2, dtype=torch.float16, device="cuda"))
