@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
   uint4 xv[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; i++)
-    if (has(i)) xv[i] = *reinterpret_cast<const uint4*>(x + r * D + (lane + 64 * i) * 8);
+    if (has(i)) xv[i] = ld_nt16(x + r * D + (lane + 64 * i) * 8);
 
   int fin = 1;
   for (int c = threadIdx.x; c < nchunk; c += kRowThreads) {
@@ -182,8 +182,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(f[i][j] / gs);
         }
-        *reinterpret_cast<uint2*>(q + r * D + c * 8) =
-            make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7]));
+        st_nt8(q + r * D + c * 8, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
       }
     }
     if (lane == 0) s[r] = gs;
@@ -204,7 +203,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
       }
       if constexpr (!QUANT) {
         const uint4 packed = finite ? narrow8x<DT, true>(o) : narrow8x<DT, false>(o);
-        *reinterpret_cast<uint4*>(y + r * D + c * 8) = packed;
+        st_nt16(y + r * D + c * 8, packed);
       } else {
         float peak = 0.0f;
         if (__builtin_expect(finite, 1) && DT == HN_DTYPE_BF16) {
@@ -237,8 +236,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(o[j] / gs);
         }
-        *reinterpret_cast<uint2*>(q + r * D + c * 8) =
-            make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7]));
+        st_nt8(q + r * D + c * 8, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
         // all 16 lanes of the group store the same scale to the same address (no divergent branch)
         s[r * (D / 128) + c / 16] = gs;
       }
@@ -309,8 +307,8 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __r
   const int64_t D = (int64_t)cpr * 8;
   for (int64_t r = (int64_t)blockIdx.y * kGrRows + threadIdx.y; r < rows; r += (int64_t)gridDim.y * kGrRows) {
     const int64_t b = L == rows ? 0 : r / L;  // one batch: no division
-    const uint4 xv = *reinterpret_cast<const uint4*>(x + r * D + c * 8);
-    const uint4 yy = *reinterpret_cast<const uint4*>(yv + r * D + c * 8);
+    const uint4 xv = ld_nt16(x + r * D + c * 8);
+    const uint4 yy = ld_nt16(yv + r * D + c * 8);
     const uint4 gv = *reinterpret_cast<const uint4*>(gate + b * D + c * 8);
     float a[8], bb[8], g[8], o[8], fr[8];
     widen8<DT>(xv, a);
@@ -331,7 +329,7 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const uint16_t* __r
     uint4 packed;
     if (__builtin_expect(nan, 0)) packed = narrow8x<DT, false>(o);
     else packed = narrow8x<DT, true>(o);
-    *reinterpret_cast<uint4*>(out + r * D + c * 8) = packed;
+    st_nt16(out + r * D + c * 8, packed);
   }
 }
 
@@ -376,7 +374,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
     r = r32;
     c = (int)(t - r32 * (uint32_t)cpr);
   }
-  const uint4 v = *reinterpret_cast<const uint4*>(q + r * ldq + c * 16);
+  const uint4 v = ld_nt16(q + r * ldq + c * 16);
   const float sc = s[r * lds];
   const float off = -128.0f * sc;
   const uint32_t w[4] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u, v.w ^ 0x80808080u};
@@ -422,7 +420,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
   const int64_t bl = hh / H, h = hh - bl * H;
   const int64_t token = bl % L;
   float f[8];
-  widen8<HN_DTYPE_BF16>(*reinterpret_cast<const uint4*>(x + bl * ldx + h * D + j * 8), f);
+  widen8<HN_DTYPE_BF16>(ld_nt16(x + bl * ldx + h * D + j * 8), f);
   float se = 0.0f, so = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; i += 2) {
@@ -450,7 +448,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
       o[i + 1] = no;
     }
   }
-  if (live) *reinterpret_cast<uint4*>(y + hh * D + j * 8) = narrow8<HN_DTYPE_BF16>(o);
+  if (live) st_nt16(y + hh * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -470,7 +468,7 @@ __global__ __launch_bounds__(256) void pixelumm_qk_kernel(const uint16_t* __rest
   const int64_t hh = live ? hg : 0;
   const int64_t t = hh / H, h = hh - t * H;
   float f[8];
-  widen8<HN_DTYPE_BF16>(*reinterpret_cast<const uint4*>(x + t * ldx + h * D + j * 8), f);
+  widen8<HN_DTYPE_BF16>(ld_nt16(x + t * ldx + h * D + j * 8), f);
   float sq = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; i++) sq = __builtin_fmaf(f[i], f[i], sq);
@@ -493,7 +491,7 @@ __global__ __launch_bounds__(256) void pixelumm_qk_kernel(const uint16_t* __rest
     const float p = __shfl(v[i], (threadIdx.x & 63) ^ partner_xor, 64);
     o[i] = first ? v[i] * c[i] - p * s[i] : v[i] * c[i] + p * s[i];
   }
-  if (live) *reinterpret_cast<uint4*>(y + hh * D + j * 8) = narrow8<HN_DTYPE_BF16>(o);
+  if (live) st_nt16(y + hh * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
 }
 
 }  // namespace hn

@@ -147,6 +147,21 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
   return __builtin_amdgcn_perm(cd, ab, 0x05040100u);                                // [ab.b0, ab.b1, cd.b0, cd.b1]
 }
 
+// Streamed accesses (each byte read or written once per launch): non-temporal, so the stream does not
+// displace cached data that is reused (per-batch factors, tables).  A 16-byte copy over 1 GiB buffers
+// runs at ~6.5 TB/s this way against ~6.2 TB/s with plain loads and stores.
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ void st_nt16(void* p, uint4 v) {
+  __builtin_nontemporal_store(v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, reinterpret_cast<v4i*>(p));
+}
+__device__ __forceinline__ void st_nt8(void* p, uint2 v) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store(v2i{(int)v.x, (int)v.y}, reinterpret_cast<v2i*>(p));
+}
+
 // fp32 pair -> packed bf16 pair, round to nearest even, with the hardware conversion (v_cvt_pk_bf16_f32).
 // It equals f32_to_bf16_bits for every non-NaN input; NaNs keep their sign and payload bits (quieted)
 // instead of becoming 0x7FC0, so callers use it where the values are known to be finite.

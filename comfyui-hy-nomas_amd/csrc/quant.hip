@@ -15,8 +15,8 @@ template <int DT>
 struct Chunk8 {
   uint4 v[DT == HN_DTYPE_F32 ? 2 : 1];
   __device__ __forceinline__ void load(const char* p) {
-    v[0] = *reinterpret_cast<const uint4*>(p);
-    if constexpr (DT == HN_DTYPE_F32) v[1] = *reinterpret_cast<const uint4*>(p + 16);
+    v[0] = ld_nt16(p);
+    if constexpr (DT == HN_DTYPE_F32) v[1] = ld_nt16(p + 16);
   }
   __device__ __forceinline__ void widen(float* f) const {
     if constexpr (DT == HN_DTYPE_F32) {
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kG128Threads) void quant_g128_kernel(const char* __
     float sc;
     const uint2 codes = encode8_group<DT, KIND, ROUND>(f, peak, sc);
     if (live[u]) {
-      *reinterpret_cast<uint2*>(q + row[u] * ldq + grp[u] * 128 + lane16 * 8) = codes;
+      st_nt8(q + row[u] * ldq + grp[u] * 128 + lane16 * 8, codes);
       if (lane16 == 0) s[row[u] * lds + grp[u]] = sc;
     }
   }
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kRowThreads) void quant_row_kernel(const char* __re
     if (c < nchunk) {
       float f[8];
       chunk[i].widen(f);
-      *reinterpret_cast<uint2*>(q + r * ldq + c * 8) = encode8_group<DT, KIND, ROUND>(f, peak, sc);
+      st_nt8(q + r * ldq + c * 8, encode8_group<DT, KIND, ROUND>(f, peak, sc));
     }
   }
   if (lane == 0) s[r * lds] = sc;  // lane 0 always owns chunk 0 (K >= 128)
