@@ -352,9 +352,10 @@ static int launch_gated_residual(const void* x, const void* y, const void* gate,
 
 // ---------------------------------------------------------------------------------------------
 // Row-scaled int8 dequantization: out[r, :] = dtype(float(q[r, :]) * s[r])      (world.py:93-94)
-// One thread per 16 codes (one 16-byte load).  A code b (as an unsigned byte after flipping its sign
-// bit) is q = b - 128, so q * s = fma(b, s, -128 s) with -128 s exact: the one rounding of the product,
-// from the single-instruction unsigned byte conversion.
+// One thread per 8 codes: an 8-byte load and, for 2-byte outputs, one 16-byte store, so each store
+// instruction writes 1 KB of consecutive output and the stream can bypass the caches.  A code b (as an
+// unsigned byte after flipping its sign bit) is q = b - 128, so q * s = fma(b, s, -128 s) with -128 s
+// exact: the one rounding of the product, from the single-instruction unsigned byte conversion.
 template <int DT, bool WIDE>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
                                                            const float* __restrict__ s, int64_t lds,
@@ -374,31 +375,26 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
     r = r32;
     c = (int)(t - r32 * (uint32_t)cpr);
   }
-  const uint4 v = ld_nt16(q + r * ldq + c * 16);
+  const uint2 v = ld_nt8(q + r * ldq + c * 8);
   const float sc = s[r * lds];
   const float off = -128.0f * sc;
-  const uint32_t w[4] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u, v.z ^ 0x80808080u, v.w ^ 0x80808080u};
-  float f[16];
+  const uint32_t w[2] = {v.x ^ 0x80808080u, v.y ^ 0x80808080u};
+  float f[8];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < 2; k++) {
     f[4 * k + 0] = __builtin_fmaf((float)(w[k] & 0xffu), sc, off);  // v_cvt_f32_ubyte0..3
     f[4 * k + 1] = __builtin_fmaf((float)((w[k] >> 8) & 0xffu), sc, off);
     f[4 * k + 2] = __builtin_fmaf((float)((w[k] >> 16) & 0xffu), sc, off);
     f[4 * k + 3] = __builtin_fmaf((float)(w[k] >> 24), sc, off);
   }
   if constexpr (DT == HN_DTYPE_F32) {
-    float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + r * ldo + c * 16);
-#pragma unroll
-    for (int k = 0; k < 4; k++) o[k] = make_float4(f[4 * k], f[4 * k + 1], f[4 * k + 2], f[4 * k + 3]);
+    float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + r * ldo + c * 8);
+    o[0] = make_float4(f[0], f[1], f[2], f[3]);
+    o[1] = make_float4(f[4], f[5], f[6], f[7]);
   } else {
-    uint4* o = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + c * 16);
-    if (__builtin_expect(sc == sc, 1)) {  // a NaN scale takes the software rounding (torch's NaN code)
-      o[0] = narrow8x<DT, true>(f);
-      o[1] = narrow8x<DT, true>(f + 8);
-    } else {
-      o[0] = narrow8x<DT, false>(f);
-      o[1] = narrow8x<DT, false>(f + 8);
-    }
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + r * ldo + c * 8;
+    if (__builtin_expect(sc == sc, 1)) st_nt16(o, narrow8x<DT, true>(f));
+    else st_nt16(o, narrow8x<DT, false>(f));  // a NaN scale takes the software rounding (torch's NaN code)
   }
 }
 
@@ -591,7 +587,7 @@ extern "C" int hn_dequantize_rows(const int8_t* q, int64_t ldq, const float* s, 
   HN_REQUIRE(q && s && out, "hn_dequantize_rows: null pointer");
   HN_REQUIRE(aligned16(q) && aligned16(out), "hn_dequantize_rows: codes and output must be 16-byte aligned");
   if (rows == 0) return HN_OK;
-  const int64_t cpr = D / 16, n = rows * cpr;
+  const int64_t cpr = D / 8, n = rows * cpr;
   HN_REQUIRE(cpr <= 0x7fffffff && (n + 255) / 256 <= 0x7fffffff, "hn_dequantize_rows: too large");
   const unsigned blocks = (unsigned)((n + 255) / 256);
   hipStream_t st = (hipStream_t)stream;

@@ -154,6 +154,11 @@ __device__ __forceinline__ uint4 ld_nt16(const void* p) {
   const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
   return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
 }
+__device__ __forceinline__ uint2 ld_nt8(const void* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const v2i v = __builtin_nontemporal_load(reinterpret_cast<const v2i*>(p));
+  return make_uint2((uint32_t)v[0], (uint32_t)v[1]);
+}
 __device__ __forceinline__ void st_nt16(void* p, uint4 v) {
   __builtin_nontemporal_store(v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, reinterpret_cast<v4i*>(p));
 }
