@@ -276,6 +276,7 @@ def elementwise(dev, gen, steps, warmup):
         "gated_residual": (lambda s: fused.gated_residual(s[0], s[1], gate), 6.0),
         "gated_residual_frames": (lambda s: fused.gated_residual_frames(s[0], s[1], gate, frames), 6.0),
         "adaln_quant": (lambda s: kernels.adaln_quant(s[0], shift, scale), 3.0 + 4.0 / 128),
+        "adaln_quant_per_token": (lambda s: kernels.adaln_quant(s[0], shift, scale, group=None), 3.0 + 4.0 / HIDDEN),
         "quantize_g128": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN)), 3.0 + 4.0 / 128),
         "quantize_per_token": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN), "int8", None),
                                3.0 + 4.0 / HIDDEN),
