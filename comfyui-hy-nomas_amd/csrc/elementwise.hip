@@ -164,9 +164,9 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
       }
     }
     peak = wave_max_nonneg(peak);
-    const bool fast = fast_group(peak);
+    const bool fast = fast_group_i8(peak);
     const float gs = fast ? int8_scale_fast(peak) : int8_scale(peak);
-    const FastDiv<false> div(gs);
+    const FastDivI8 div(gs);
 #pragma unroll
     for (int i = 0; i < CPL; i++) {
       const int c = lane + 64 * i;
@@ -223,9 +223,9 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
         peak = row16_max_nonneg(peak);
         float gs;
         int cd[8];
-        if (__builtin_expect(fast_group(peak), 1)) {
+        if (__builtin_expect(fast_group_i8(peak), 1)) {
           gs = int8_scale_fast(peak);
-          const FastDiv<false> div(gs);
+          const FastDivI8 div(gs);
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             const float v = div(o[j]);

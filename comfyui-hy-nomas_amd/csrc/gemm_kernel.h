@@ -706,8 +706,8 @@ void block_gemm_kernel(const GemmArgs a) {
             }
           peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));
           const float gs = KIND == HN_KIND_FP8 ? fp8_scale(peak) : int8_scale(peak);
-          const bool fast = fast_group(peak);  // h holds bf16 values: the exact three-op quotient applies
-          const FastDiv<KIND == HN_KIND_FP8> div(gs);
+          const bool fast = FastQuot<KIND>::ok(peak);  // h holds bf16 values: the exact fast quotient applies
+          const typename FastQuot<KIND>::Div div(gs);
           const int ml = erow_m + j * 32;
           if (ml < mrem) {
             uint8_t* o = reinterpret_cast<uint8_t*>(a.out) + em0 * a.ldo + en0 / 2;
@@ -816,9 +816,9 @@ void block_gemm_kernel(const GemmArgs a) {
             for (int r = 0; r < 16; r++) peak = __builtin_fmaxf(peak, __builtin_fabsf(MF::get(acc[i][j], r)));
           peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));
           const float gs = int8_scale(peak);
-          // the GELU outputs are bf16 values: the exact three-op quotient applies to the group (hn_common.h)
-          const bool fast = fast_group(peak);
-          const FastDiv<false> div(gs);
+          // the GELU outputs are bf16 values: the exact two-op int8 quotient applies to the group (hn_common.h)
+          const bool fast = fast_group_i8(peak);
+          const FastDivI8 div(gs);
           if (m_ok) {
             int8_t* o = reinterpret_cast<int8_t*>(a.out) + em0 * a.ldo + en0;
 #pragma unroll

@@ -113,6 +113,35 @@ struct FastDiv {
 
 __device__ __forceinline__ bool fast_group(float peak) { return peak >= 0x1p-80f; }
 
+// int8 quotients in two VALU ops per value: with r = RN(1 / s) as above and its remainder
+// rl = RN(fma(-s, r, 1) * r), q = fma(x, r, x * rl).  For every bf16 absmax 2^-80 <= peak < 2^100 and every
+// bf16 |x| <= peak, both signs, q gives the same int8 code as IEEE x / s for both roundings (exhaustive CPU
+// check).  From 2^100 up, rl falls into the subnormals and loses the bits it carries, so those groups
+// divide.  (x * r alone is not enough: it changes codes next to exact .5 ties, e.g. x = peak / 2.)
+struct FastDivI8 {
+  float r, rl;
+  __device__ __forceinline__ explicit FastDivI8(float scale) {
+    const float r0 = __builtin_amdgcn_rcpf(scale);
+    r = __builtin_fmaf(__builtin_fmaf(-r0, scale, 1.0f), r0, r0);
+    rl = __builtin_fmaf(-scale, r, 1.0f) * r;
+  }
+  __device__ __forceinline__ float operator()(float x) const { return __builtin_fmaf(x, r, x * rl); }
+};
+
+__device__ __forceinline__ bool fast_group_i8(float peak) { return peak >= 0x1p-80f && peak < 0x1p100f; }
+
+// The fast quotient and its group condition for each code kind: two ops for int8, three for e4m3.
+template <int KIND>
+struct FastQuot {
+  using Div = FastDivI8;
+  __device__ __forceinline__ static bool ok(float peak) { return fast_group_i8(peak); }
+};
+template <>
+struct FastQuot<HN_KIND_FP8> {
+  using Div = FastDiv<true>;
+  __device__ __forceinline__ static bool ok(float peak) { return fast_group(peak); }
+};
+
 // Code of y = x / scale with |x| <= the group's peak (so |y| <= 127 * (1 + 2^-22) and no clamp is needed):
 // round half away from zero as trunc(y + copysign(0.5, y)); NaN gives 0.
 __device__ __forceinline__ int round_half_away_i8_inrange(float y) {

@@ -32,13 +32,13 @@ struct Chunk8 {
 };
 
 // Codes of 8 values with one scale; returns them packed in 8 bytes.  FAST: bf16-valued inputs in a group
-// with fast_group(peak) -- the three-op exact quotient, and (int8) no clamp since |x| <= peak.  Otherwise an
+// with FastQuot<KIND>::ok(peak) -- the exact fast quotient, and (int8) no clamp since |x| <= peak.  Otherwise an
 // IEEE division and the clamped rounding.
 template <int KIND, int ROUND, bool FAST>
 __device__ __forceinline__ uint2 encode8(const float* f, float scale) {
   int c[8];
   if constexpr (FAST) {
-    const FastDiv<KIND == HN_KIND_FP8> div(scale);
+    const typename FastQuot<KIND>::Div div(scale);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float y = div(f[i]);
@@ -58,11 +58,11 @@ __device__ __forceinline__ uint2 encode8(const float* f, float scale) {
 }
 
 // Scale and codes of one group from its absmax `peak` (non-negative, NaN-free).  bf16 inputs in a group
-// with fast_group(peak) use the three-op quotients (hn_common.h); other groups and inputs divide.
+// with FastQuot<KIND>::ok(peak) use the fast exact quotients (hn_common.h); other groups and inputs divide.
 template <int DT, int KIND, int ROUND>
 __device__ __forceinline__ uint2 encode8_group(const float* f, float peak, float& scale) {
   if constexpr (DT == HN_DTYPE_BF16) {
-    if (__builtin_expect(fast_group(peak), 1)) {
+    if (__builtin_expect(FastQuot<KIND>::ok(peak), 1)) {
       scale = KIND == HN_KIND_INT8 ? int8_scale_fast(peak) : fp8_scale_fast(peak);
       return encode8<KIND, ROUND, true>(f, scale);
     }

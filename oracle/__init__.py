@@ -75,6 +75,8 @@ def lib():
     l.hno_swiglu.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i64, ctypes.c_void_p]
     l.hno_check_fast_division.argtypes = [ctypes.c_int, _i64, _i64]
     l.hno_check_fast_division.restype = ctypes.c_int64
+    l.hno_check_fast_division2.argtypes = [_i64, _i64, ctypes.c_int]
+    l.hno_check_fast_division2.restype = ctypes.c_int64
     l.hno_check_scale_division.argtypes = []
     l.hno_check_scale_division.restype = ctypes.c_int64
     l.hno_check_reciprocal_refinement.argtypes = []

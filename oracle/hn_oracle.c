@@ -390,6 +390,36 @@ int64_t hno_check_fast_division(int fp8, int64_t peak_begin, int64_t peak_end) {
     return bad;
 }
 
+/* Two-operation form of the same int8 quotient: with r = RN(1 / s) and rl = RN(fma(-s, r, 1) * r),
+ * q = fma(x, r, x * rl).  The device uses it for int8 groups whose bf16 absmax `peak` satisfies
+ * 2^-80 <= peak < 2^100 (above that rl is subnormal and loses the bits it carries); other groups
+ * divide.  Checks every such bf16 peak and every bf16 |x| <= peak, both signs, against the reference
+ * rule (IEEE x / s, floor / ceil or rint, clamped) for both roundings.  Returns the mismatches.
+ * `drop_rl` plants a mistake (rl = 0, i.e. q = x * r) so a test can see the check catch it. */
+int64_t hno_check_fast_division2(int64_t peak_begin, int64_t peak_end, int drop_rl) {
+    int64_t bad = 0;
+    #pragma omp parallel for reduction(+:bad) schedule(dynamic, 64)
+    for (int64_t pbi = peak_begin; pbi < peak_end; pbi++) {
+        uint32_t pb = (uint32_t)pbi;
+        float p = float_of(pb << 16);
+        if (!(p >= 0x1p-80f && p < 0x1p100f)) continue;
+        float s = int8_scale(p);
+        float r = 1.0f / s;
+        float rl = drop_rl ? 0.0f : fmaf(-s, r, 1.0f) * r;
+        for (uint32_t xb = 0; xb <= pb; xb++) {
+            for (int sign = 0; sign < 2; sign++) {
+                float x = float_of((xb << 16) | (sign ? 0x80000000u : 0u));
+                float ref = x / s;
+                float got = fmaf(x, r, x * rl);
+                int fast_away = (int)(got + copysignf(0.5f, got));
+                int fast_even = (int)rintf(got);
+                if (fast_away != ref_code_half_away(ref) || fast_even != ref_code_half_even(ref)) bad++;
+            }
+        }
+    }
+    return bad;
+}
+
 /* The device's reciprocal of a group scale s (peaks >= 2^-80): r0 = v_rcp_f32(s), accurate to 1 ulp,
  * refined by one Newton step r1 = fma(fma(-r0, s, 1), r0, r0).  For every bf16 peak >= 2^-80 and both
  * scale kinds, this checks that every r0 within +-2 ulp of RN(1 / s) refines to exactly RN(1 / s), so

@@ -132,6 +132,16 @@ def test_fast_division_lemma_exhaustive():
     assert lib.hno_check_fast_division(1, 1, 0x7F80) == 0
 
 
+def test_two_op_division_lemma_exhaustive():
+    """The int8 quantizers' two-operation quotient fma(x, r, x * rl) (r = RN(1 / s), rl = RN(fma(-s, r, 1) * r))
+    gives the reference's int8 codes, both roundings, for every bf16 absmax in [2^-80, 2^100) and every bf16
+    x with |x| <= absmax, both signs.  A planted error (rl dropped) must be caught: x * r alone changes codes
+    next to exact .5 ties."""
+    lib = oracle.lib()
+    assert lib.hno_check_fast_division2(1, 0x7F80, 0) == 0
+    assert lib.hno_check_fast_division2(0x3F00, 0x4380, 1) > 0  # peaks 0.5 .. 256 with the planted error
+
+
 def test_reciprocal_refinement_exhaustive():
     """The device's 1 / scale: any hardware reciprocal within 2 ulp, refined by one FMA Newton step, is the
     correctly rounded reciprocal for every bf16 peak >= 2^-80 (int8 and fp8 scales)."""
