@@ -430,7 +430,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the quantized linear path is single-GPU here (token-parallel "
-              "sharding needs no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "sharding needs no exchange between GPUs). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

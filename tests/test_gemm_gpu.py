@@ -95,7 +95,7 @@ def test_int8_gemm_bit_exact(dev, m, n, k, per_channel, with_bias):
     got = out.cpu()
     diff = (got != ref_bf16).nonzero()
     assert diff.numel() == 0, f"{len(diff)} outputs differ from the oracle, first {diff[:3].tolist()}"
-    # and the north-star bar against the dequantized-operand product
+    # and the 1e-2 max-abs-rel bar against the product of the dequantized operands
     assert max_abs_rel(got.float().numpy(), fp64_dequant_product(qa, sa, w.numpy(), sw.numpy(), bias)) < 1e-2
 
 

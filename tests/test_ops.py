@@ -105,7 +105,7 @@ def test_set_weight_requantizes_and_int8_weights_yields_the_codes():
 @pytest.mark.gpu
 def test_int8_mode_runs_the_matrix_core_path(dev):
     """int8 mode on a device input: bit-identical to block_linear (per-token-and-group quantization + the
-    g128 GEMM), within the north-star 1e-2 of the exact path, and `fast_int8` holds."""
+    g128 GEMM), within 1e-2 max-abs-rel of the exact path, and `fast_int8` holds."""
     from hy_nomas import kernels, ops
 
     print("ops.Linear int8 mode", flush=True)
