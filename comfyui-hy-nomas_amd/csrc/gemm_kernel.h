@@ -249,8 +249,9 @@ void block_gemm_kernel(const GemmArgs a) {
   static_assert(!WBLK || (G128 && (TN * 32) % 128 == 0 && BN % 128 == 0), "block weight scales");
   // RESCALE (fp8 with block weight scales): no separate fp32 running sum.  The matrix core accumulates
   // every group straight into acc, kept in units of the current group's scale product: at each group
-  // boundary acc *= ss_g / ss_{g+1} (one VALU op per output), and the epilogue multiplies by the last
-  // group's ss.  ss_g = sa[m, g] * sw[block, g] is positive (both quantizers floor their scales).
+  // boundary acc *= ss_g / ss_{g+1} (one VALU op per output, issued block by block between the next
+  // group's first products), and the epilogue multiplies by the last group's ss.
+  // ss_g = sa[m, g] * sw[block, g] is positive (both quantizers floor their scales).
   constexpr bool RESCALE = G128 && WBLK && KIND == HN_KIND_FP8;
   // Epilogue staging of 2-byte outputs, one block of 32 tokens at a time: each wave transposes its
   // 32 x BNW sub-tile through LDS (token-major rows padded by 16 bytes) so the stores are full 16-byte
@@ -468,11 +469,28 @@ void block_gemm_kernel(const GemmArgs a) {
     read_frags(0, smem + SCR, 0);
 
     // products of weight fragments [i0, i1) with every activation fragment of register set `set`
-    auto mfma_rows = [&](int set, int i0, int i1) __attribute__((always_inline)) {
+    // rs (RESCALE, a stage's first slice): each accumulator block is moved to this group's scale product
+    // just before its first product of the stage, 16 multiplies per block interleaved with the matrix core
+    auto mfma_rows = [&](int set, int i0, int i1, const float* rs = nullptr) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = i0; i < i1; i++)
 #pragma unroll
-        for (int j = 0; j < TM; j++) acc[i][j] = MF::run(fa[set][i], fb[set][j], acc[i][j]);
+        for (int j = 0; j < TM; j++) {
+          if (rs) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] *= rs[j];
+          }
+          acc[i][j] = MF::run(fa[set][i], fb[set][j], acc[i][j]);
+        }
+      if (rs) {
+#pragma unroll
+        for (int i = i0; i < i1; i++)
+#pragma unroll
+          for (int j = 0; j < TM; j++) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+      }
     };
     // One K stage (kt, in buffer `buf`).  The schedule is pinned with scheduling barriers (address
     // arithmetic may still move): each slice issues the next slice's fragment reads right after its
@@ -488,15 +506,31 @@ void block_gemm_kernel(const GemmArgs a) {
     auto stage_body = [&](int kt, int buf, auto mode_c) __attribute__((always_inline)) {
       constexpr int MODE = decltype(mode_c)::value;
       const char* stage = smem + SCR + buf * STAGE;
+      // RESCALE: the factor from the previous group's scale product to this one's (1 at the tile's first
+      // stage).  The previous group's scales are still in their ring slot: stage kt + 2 refills it only
+      // after this stage's barrier.
+      float rs[TM];
+      if constexpr (RESCALE) {
+        static_assert(STAGES_PER_GROUP == 1, "one group per stage");
+        const float* sp = reinterpret_cast<const float*>(smem + ((kt + NS) % (NS + 1)) * SC_BYTES);
+        const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
+        const float swp = sp[wn * TN * 32], swc = sc[wn * TN * 32];
+#pragma unroll
+        for (int j = 0; j < TM; j++) {
+          const float rho = (sp[BN + wrow_m + j * 32] * swp) / (sc[BN + wrow_m + j * 32] * swc);
+          rs[j] = kt > 0 ? rho : 1.0f;
+        }
+      }
 #pragma unroll
       for (int s = 0; s < SLICES; s++) {
         const int cur = s & 1;
+        const float* rsc = RESCALE && s == 0 ? rs : nullptr;
         if (s + 1 < SLICES) {
-          mfma_rows(cur, 0, 1);
+          mfma_rows(cur, 0, 1, rsc);
           __builtin_amdgcn_sched_barrier(0x6);
           read_frags(cur ^ 1, stage, s + 1);
           __builtin_amdgcn_sched_barrier(0x6);
-          mfma_rows(cur, 1, TN);
+          mfma_rows(cur, 1, TN, rsc);
           __builtin_amdgcn_sched_barrier(0x6);
         } else if constexpr (MODE == 2) {
           mfma_rows(cur, 0, TN);
@@ -525,24 +559,11 @@ void block_gemm_kernel(const GemmArgs a) {
         }
       }
       if constexpr (RESCALE) {
-        static_assert(STAGES_PER_GROUP == 1, "one group per stage");
-        const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
-        const float swb = sc[wn * TN * 32];  // the wave's one weight scale
         if constexpr (MODE == 2) {
+          const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
+          const float swb = sc[wn * TN * 32];  // the wave's one weight scale
 #pragma unroll
           for (int j = 0; j < TM; j++) ss_last[j] = sc[BN + wrow_m + j * 32] * swb;
-        } else {
-          // the next group's scales landed with stage kt + 1 (published by this stage's barrier)
-          const float* sn = reinterpret_cast<const float*>(smem + ((kt + 1) % (NS + 1)) * SC_BYTES);
-          const float swn = sn[wn * TN * 32];
-#pragma unroll
-          for (int j = 0; j < TM; j++) {
-            const float rho = (sc[BN + wrow_m + j * 32] * swb) / (sn[BN + wrow_m + j * 32] * swn);
-#pragma unroll
-            for (int i = 0; i < TN; i++)
-#pragma unroll
-              for (int r = 0; r < 16; r++) acc[i][j][r] *= rho;
-          }
         }
       } else if constexpr (G128) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
