@@ -75,6 +75,26 @@ def test_quant_ties_and_zero_groups(dev):
         check_quant(x, dev, "int8", group, "half_even")
 
 
+def test_quant_group_magnitudes_across_the_fast_quotient_range(dev):
+    """int8 groups whose absmax lies on both sides of the two-op quotient's range [2^-80, 2^100) and at the
+    ends of the float range.  Each first group holds peak * (2k + 1) / 254 rounded to bf16 (next to the
+    half-away ties of codes k), each second group random values of the same magnitude.  Both roundings,
+    one scale per group and one per token, bit-exact against the oracle."""
+    g = seeded(17)
+    rows = []
+    for e in (-126, -100, -81, -80, -79, -1, 0, 99, 100, 101, 120, 126):
+        peak = 1.5 * 2.0 ** e
+        ties = torch.tensor([peak * (2 * k + 1) / 254 for k in range(-64, 63)] + [peak])
+        rand = torch.randn(128, generator=g) * (peak / 4)
+        rand[0] = -peak
+        rows.append(torch.cat([ties, rand]))
+    x = torch.stack(rows).to(torch.bfloat16)
+    assert torch.isfinite(x.float()).all()
+    for group in (128, None):
+        check_quant(x, dev, "int8", group)
+        check_quant(x, dev, "int8", group, "half_even")
+
+
 def test_quant_strided_rows(dev):
     from hy_nomas import kernels
 
