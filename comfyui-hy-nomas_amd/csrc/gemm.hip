@@ -36,7 +36,7 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
   a.tiles_n = (int)tn;
   const int64_t slots = (int64_t)cu_count() * (WPE * 4 / (WN * WM));
   const int64_t grid = tm * tn < slots ? tm * tn : slots;
-  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS, WBLK, false, WPE>),
+  hipLaunchKernelGGL((block_gemm_kernel<KIND, EPI, G128, WN, WM, TN, TM, OUT_DT, BK, NS, WBLK, WPE>),
                      dim3((unsigned)grid), dim3(WN * WM * 64), 0, st, a);
   return HN_LAUNCH_CHECK("block_gemm_kernel");
 }

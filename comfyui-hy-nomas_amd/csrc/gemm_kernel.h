@@ -216,7 +216,7 @@ __device__ __forceinline__ uint32_t cvt2_out(float a, float b) {
 // The first stage of the next tile is issued before the current tile's epilogue, so its load latency
 // hides behind the epilogue and the epilogue's stores drain while it lands.
 template <int KIND, int EPI, bool G128, int WN, int WM, int TN, int TM, int OUT_DT, int BK, int NS, bool WBLK,
-          bool AV = false, int WPE = WN * WM / 4>
+          int WPE = WN * WM / 4>
 __global__ __launch_bounds__(WN* WM * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void block_gemm_kernel(const GemmArgs a) {
   using MF = Mfma<KIND>;
@@ -348,37 +348,19 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     }
   };
-  // AV: the activation tile goes through registers (global loads into astg, then LDS writes once they
-  // land) while the weight tile streams straight into LDS; the two paths run side by side.
-  v4i astg[AV ? B_KB : 1];
   auto issue_stage = [&](int kt, int buf) {
     char* base = smem + SCR + buf * STAGE;
     const uint8_t* wk = wbase + (int64_t)kt * BK;
     const uint8_t* ak = abase + (int64_t)kt * BK;
-    if constexpr (AV) {
-#pragma unroll
-      for (int u = 0; u < B_KB; u++) astg[u] = *reinterpret_cast<const v4i*>(ak + aoff[u]);
-    }
 #pragma unroll
     for (int u = 0; u < A_KB; u++) g2lds16(wk + woff[u], base + (wave + NW * u) * 1024);
-    if constexpr (!AV) {
 #pragma unroll
-      for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
-    }
+    for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
 #pragma unroll
     for (int u = 0; u < SC_PER_WAVE; u++)
       g2lds4(scbase[u] + kt / STAGES_PER_GROUP + scoff[u], smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
   };
 
-  // AV: the activation tile of a landed stage, from registers into buffer `buf` (same LDS layout as the
-  // direct loads: lane i's 16 bytes at block base + 16 i)
-  auto commit_stage = [&](int buf) {
-    if constexpr (AV) {
-      char* base = smem + SCR + buf * STAGE + A_BYTES;
-#pragma unroll
-      for (int u = 0; u < B_KB; u++) *reinterpret_cast<v4i*>(base + (wave + NW * u) * 1024 + lane * 16) = astg[u];
-    }
-  };
 
   const int nk = (int)(a.K / BK);
   const int wrow_n = wn * TN * 32 + (lane & 31);  // this lane's A-fragment row within the weight tile
@@ -449,7 +431,6 @@ void block_gemm_kernel(const GemmArgs a) {
     // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging and
     // operand reads of the previous epilogue are done, so buffer 1 and the operand area are free
     wait_vmcnt<0>();
-    commit_stage(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     barrier();
     if constexpr (EPI != HN_EPI_ACC32) {
@@ -504,7 +485,7 @@ void block_gemm_kernel(const GemmArgs a) {
     // (0 there is 0.5 % and 3 % slower).
     constexpr int PRE = G128 ? 1 : 0;
     constexpr int POST_MFMA = (TN - PRE) * TM;
-    constexpr int VM_LOADS = A_KB + (AV ? 0 : B_KB) + SC_PER_WAVE;
+    constexpr int VM_LOADS = A_KB + B_KB + SC_PER_WAVE;
     constexpr int VM_PER = (VM_LOADS + POST_MFMA - 1) / POST_MFMA;  // POST_MFMA >= TM > 0
     auto stage_body = [&](int kt, int buf, auto mode_c) __attribute__((always_inline)) {
       constexpr int MODE = decltype(mode_c)::value;
@@ -544,7 +525,6 @@ void block_gemm_kernel(const GemmArgs a) {
           // stage kt + 1 (the only loads in flight) has landed for this wave and its reads of stage kt
           // are complete; the barrier publishes both facts, then stage kt + 2 may refill `buf`
           wait_vmcnt<0>();
-          commit_stage(buf ^ 1);
           __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
           barrier();
           __builtin_amdgcn_sched_barrier(0);
