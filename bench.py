@@ -493,8 +493,10 @@ def main():
                                "activations x per-channel int8 weights, bf16 bias, bf16 out",
                    "M": M, "hidden": HIDDEN, "ops_per_step": ops, "frac_int8_peak": round(value / PEAK_INT8_TOPS, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TOPS",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 3), "traffic": TRAFFIC_BYTES_PER_STEP,
-                     "traffic_unit": "bytes per step of 4 GEMM launches (rocprofv3 FETCH_SIZE+WRITE_SIZE)",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 3), "traffic": TRAFFIC_BYTES_PER_STEP / len(STACK),
+                     "traffic_unit": "bytes per launch, the average of the four GEMMs of a step (rocprofv3 "
+                                     "FETCH_SIZE x2.0 + WRITE_SIZE x1.0 per launch; FETCH_SIZE includes "
+                                     "Infinity Cache hits)",
                      "kernel": "block_gemm_kernel (int8, per-token)", "per_gemm": per_gemm},
     }
     if not args.no_extra:
