@@ -1,5 +1,7 @@
 // Dispatch and C ABI of the block-scaled 8-bit GEMM (hy_nomas/kernels.py:152-170, block_gemm).
 // The kernel template and its design notes are in gemm_kernel.h.
+#include <atomic>
+
 #include "gemm_kernel.h"
 #include "skinny_kernel.h"
 
@@ -9,16 +11,17 @@ namespace hn {
 // configurations
 
 // Compute units of the current device (the persistent grid has at most one workgroup per CU).
+// The per-device cache may be filled by several host threads at once; they store the same value.
 static int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // WPE: waves per SIMD the kernel is compiled for; above WN * WM / 4, several workgroups share a CU and the
