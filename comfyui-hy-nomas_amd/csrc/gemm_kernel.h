@@ -482,7 +482,7 @@ void block_gemm_kernel(const GemmArgs a) {
     // tile's last stage (neither).
     // Weight rows multiplied before the barrier.  Per-token tiles issue all of the last slice's products
     // after it (1.7 % faster over the DiT stack); the g128 and block-scale tiles keep one row before it
-    // (0 there is 0.5 % and 3 % slower).
+    // (none there is 0.5 % and 3 % slower, two 0.4 % and 2.5 % slower).
     constexpr int PRE = G128 ? 1 : 0;
     constexpr int POST_MFMA = (TN - PRE) * TM;
     constexpr int VM_LOADS = A_KB + B_KB + SC_PER_WAVE;
