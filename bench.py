@@ -129,7 +129,7 @@ def time_launches(fns, steps, warmup, warm_s=0.0):
     return total_ms, per
 
 
-def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", warm_s=WARM_S):
+def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", warm_s=WARM_S, expand=False):
     """Headline stack.  Returns (ms/step, per-GEMM ms, total ops, [(name, K, N)])."""
     from hy_nomas import kernels
 
@@ -145,7 +145,9 @@ def gemm_stack(dev, gen, steps, warmup, group_mode="per_token", kind="int8", war
             qa, sa = kernels.quantize_activations(x, "fp8", 128)
             wf = torch.randn(n, k, generator=gen, device=dev) * 0.02
             w, sblk = pixelumm.quantize_fp8_block(wf)
-            sw = sblk   # [N/128, K/128] block scales, read directly by the GEMM
+            # [N/128, K/128] block scales, read directly by the GEMM; expand: one row per output channel,
+            # as the reference hands them to its kernel (pixelumm.py:153, repeat_interleave(128, 0))
+            sw = sblk.repeat_interleave(128, 0)[:n].contiguous() if expand else sblk
             bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
             del wf
         del x
@@ -516,6 +518,10 @@ def main():
             fp8[name] = {"ms": round(t, 4), "TFLOPS": round(2 * M * n * k / (t * 1e-3) / 1e12, 1)}
         extra["fp8_block_gemm"] = {"per_gemm": fp8, "stack_ms": round(ms_f, 4),
                                    "frac_fp8_peak": round(ops / (ms_f * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 3)}
+        log("bench: fp8 stack, block scales expanded per channel (the reference's layout)")
+        ms_e, per_e, _ = gemm_stack(dev, gen, max(5, args.steps // 2), 2, kind="fp8", expand=True)
+        extra["fp8_expanded_scales"] = {"stack_ms": round(ms_e, 4), "TFLOPS": round(ops / (ms_e * 1e-3) / 1e12, 1),
+                                        "per_gemm_ms": [round(t, 4) for t in per_e]}
         log("bench: decoder MLP (fp8, fused SwiGLU)")
         extra["decoder_mlp_fp8"] = decoder_mlp(dev, gen, max(5, args.steps // 2), 2)
         log("bench: elementwise")
