@@ -273,6 +273,14 @@ def elementwise(dev, gen, steps, warmup):
     gate = (torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
     # camera output per latent frame: 32 frames of 1024 tokens
     frames = (torch.randn(1, 32, HIDDEN, generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    # QK norms: 24 heads x 128, per-token rotary tables [M, 128] fp32 (read by every head of the token)
+    heads, hd = HIDDEN // 128, 128
+    qn_w = (torch.rand(hd, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+    ang = torch.rand(M, hd, generator=gen, device=dev) * 6.283
+    cos_t, sin_t = torch.cos(ang), torch.sin(ang)
+    wt = (torch.rand(hd // 2, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+    whw = (torch.rand(hd // 2, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+    tables_bpe = 2.0 * M * hd * 4 / n_el
     cases = {
         "adaln": (lambda s: fused.adaln(s[0], shift, scale), 4.0),
         "gated_residual": (lambda s: fused.gated_residual(s[0], s[1], gate), 6.0),
@@ -282,6 +290,10 @@ def elementwise(dev, gen, steps, warmup):
         "quantize_g128": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN)), 3.0 + 4.0 / 128),
         "quantize_per_token": (lambda s: kernels.quantize_activations(s[0].view(M, HIDDEN), "int8", None),
                                3.0 + 4.0 / HIDDEN),
+        "qk_norm_rope": (lambda s: fused.qk_norm_rope(s[0].view(1, M, heads, hd), qn_w, (cos_t, sin_t)),
+                         4.0 + tables_bpe),
+        "pixelumm_qk": (lambda s: fused.pixelumm_qk(s[0].view(1, M, heads, hd), wt, whw, cos_t, sin_t),
+                        4.0 + tables_bpe),
     }
     out = {}
     for name, (fn, bpe) in cases.items():

@@ -400,94 +400,126 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
 
 // ---------------------------------------------------------------------------------------------
 // QK RMSNorm + interleaved RoPE                                  (fused.py:65-91)
-// W = D / 8 lanes per (token, head); 64 / W heads per wavefront.
-template <int W, bool ROPE>
+// W = D / 8 lanes per head, lane j holding dims [8j, 8j + 8).  Each W-lane group normalizes G heads of
+// one token (G = 6, 4, 2 or 1, the largest that divides the head count): the weight and the token's
+// rotary rows are loaded once per group, and the group's G head rows are all in flight before the
+// first is reduced.
+template <int W, bool ROPE, int G>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ cs,
-                                                           const float* __restrict__ sn, int64_t n_heads,
+                                                           const float* __restrict__ sn, int64_t n_groups,
                                                            int64_t H, int64_t L, float eps,
                                                            uint16_t* __restrict__ y) {
   constexpr int D = W * 8;
-  const int64_t hg = ((int64_t)blockIdx.x * 256 + threadIdx.x) / W;  // (batch * token, head) index
+  const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) / W;  // (batch * token, head group) index
   const int j = threadIdx.x & (W - 1);
-  const bool live = hg < n_heads;
-  const int64_t hh = live ? hg : 0;
-  const int64_t bl = hh / H, h = hh - bl * H;
+  const bool live = grp < n_groups;
+  const int64_t gg = live ? grp : 0;
+  const int64_t per_tok = H / G;
+  const int64_t bl = gg / per_tok, h0 = (gg - bl * per_tok) * G;
   const int64_t token = bl % L;
-  float f[8];
-  widen8<HN_DTYPE_BF16>(ld_nt16(x + bl * ldx + h * D + j * 8), f);
-  float se = 0.0f, so = 0.0f;
+  float wv[8], cv[8], sv[8];
 #pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    se = __builtin_fmaf(f[i], f[i], se);
-    so = __builtin_fmaf(f[i + 1], f[i + 1], so);
-  }
+  for (int i = 0; i < 8; i++) wv[i] = w[j * 8 + i];
+  if constexpr (ROPE) {
 #pragma unroll
-  for (int m = 1; m < W; m <<= 1) {
-    se += shfl_xor_f(se, m, W);
-    so += shfl_xor_f(so, m, W);
-  }
-  const float r = 1.0f / __builtin_sqrtf((se + so) / (float)D + eps);
-  float o[8];
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) {
-    const float ne = rbf16(rbf16(f[i] * r) * w[j * 8 + i]);
-    const float no = rbf16(rbf16(f[i + 1] * r) * w[j * 8 + i + 1]);
-    if constexpr (ROPE) {
-      const float* c = cs + token * D + j * 8;
-      const float* s = sn + token * D + j * 8;
-      o[i] = ne * c[i] - no * s[i];
-      o[i + 1] = no * c[i + 1] + ne * s[i + 1];
-    } else {
-      o[i] = ne;
-      o[i + 1] = no;
+    for (int i = 0; i < 8; i++) {
+      cv[i] = cs[token * D + j * 8 + i];
+      sv[i] = sn[token * D + j * 8 + i];
     }
   }
-  if (live) st_nt16(y + hh * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+  uint4 xr[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) xr[g] = ld_nt16(x + bl * ldx + (h0 + g) * D + j * 8);
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float f[8];
+    widen8<HN_DTYPE_BF16>(xr[g], f);
+    float se = 0.0f, so = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      se = __builtin_fmaf(f[i], f[i], se);
+      so = __builtin_fmaf(f[i + 1], f[i + 1], so);
+    }
+#pragma unroll
+    for (int m = 1; m < W; m <<= 1) {
+      se += shfl_xor_f(se, m, W);
+      so += shfl_xor_f(so, m, W);
+    }
+    const float r = 1.0f / __builtin_sqrtf((se + so) / (float)D + eps);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const float ne = rbf16(rbf16(f[i] * r) * wv[i]);
+      const float no = rbf16(rbf16(f[i + 1] * r) * wv[i + 1]);
+      if constexpr (ROPE) {
+        o[i] = ne * cv[i] - no * sv[i];
+        o[i + 1] = no * cv[i + 1] + ne * sv[i + 1];
+      } else {
+        o[i] = ne;
+        o[i + 1] = no;
+      }
+    }
+    if (live) st_nt16(y + (bl * H + h0 + g) * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
 // PixelUMM split-half RMSNorm + sectioned rotate-half MRoPE, head_dim 128 (fused.py:131-175).
-// 16 lanes per (token, head); lane j holds dims [8j, 8j + 8).  T section = lanes 0-7 (rotate-half
+// 16 lanes per head, lane j holding dims [8j, 8j + 8), and G heads of one token per 16-lane group as in
+// qk_norm_rope_kernel.  T section = lanes 0-7 (rotate-half
 // partner 4 lanes away), H section = lanes 8-11, W section = lanes 12-15 (partner 2 lanes away).
+template <int G>
 __global__ __launch_bounds__(256) void pixelumm_qk_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           const float* __restrict__ wt,
                                                           const float* __restrict__ whw,
                                                           const float* __restrict__ cs,
-                                                          const float* __restrict__ sn, int64_t n_heads, int64_t H,
+                                                          const float* __restrict__ sn, int64_t n_groups, int64_t H,
                                                           float eps, uint16_t* __restrict__ y) {
   constexpr int D = 128;
-  const int64_t hg = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
+  const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) / 16;
   const int j = threadIdx.x & 15;
-  const bool live = hg < n_heads;
-  const int64_t hh = live ? hg : 0;
-  const int64_t t = hh / H, h = hh - t * H;
-  float f[8];
-  widen8<HN_DTYPE_BF16>(ld_nt16(x + t * ldx + h * D + j * 8), f);
-  float sq = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) sq = __builtin_fmaf(f[i], f[i], sq);
-  // lanes 0-7 reduce the T half, lanes 8-15 the HW half
-  sq += shfl_xor_f(sq, 1, 16);
-  sq += shfl_xor_f(sq, 2, 16);
-  sq += shfl_xor_f(sq, 4, 16);
-  const float rr = 1.0f / __builtin_sqrtf(sq / (float)(D / 2) + eps);
-  const float* wv = j < 8 ? wt + j * 8 : whw + (j - 8) * 8;
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) v[i] = f[i] * rr * wv[i];
-  const int partner_xor = j < 8 ? 4 : 2;
-  const bool first = j < 8 ? (j < 4) : ((j & 3) < 2);
-  const float* c = cs + t * D + j * 8;
-  const float* s = sn + t * D + j * 8;
-  float o[8];
+  const bool live = grp < n_groups;
+  const int64_t gg = live ? grp : 0;
+  const int64_t per_tok = H / G;
+  const int64_t t = gg / per_tok, h0 = (gg - t * per_tok) * G;
+  const float* wp = j < 8 ? wt + j * 8 : whw + (j - 8) * 8;
+  float wv[8], cv[8], sv[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    const float p = __shfl(v[i], (threadIdx.x & 63) ^ partner_xor, 64);
-    o[i] = first ? v[i] * c[i] - p * s[i] : v[i] * c[i] + p * s[i];
+    wv[i] = wp[i];
+    cv[i] = cs[t * D + j * 8 + i];
+    sv[i] = sn[t * D + j * 8 + i];
   }
-  if (live) st_nt16(y + hh * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+  const int partner_xor = j < 8 ? 4 : 2;
+  const bool first = j < 8 ? (j < 4) : ((j & 3) < 2);
+  uint4 xr[G];
+#pragma unroll
+  for (int g = 0; g < G; g++) xr[g] = ld_nt16(x + t * ldx + (h0 + g) * D + j * 8);
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float f[8];
+    widen8<HN_DTYPE_BF16>(xr[g], f);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) sq = __builtin_fmaf(f[i], f[i], sq);
+    // lanes 0-7 reduce the T half, lanes 8-15 the HW half
+    sq += shfl_xor_f(sq, 1, 16);
+    sq += shfl_xor_f(sq, 2, 16);
+    sq += shfl_xor_f(sq, 4, 16);
+    const float rr = 1.0f / __builtin_sqrtf(sq / (float)(D / 2) + eps);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = f[i] * rr * wv[i];
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float p = __shfl(v[i], (threadIdx.x & 63) ^ partner_xor, 64);
+      o[i] = first ? v[i] * cv[i] - p * sv[i] : v[i] * cv[i] + p * sv[i];
+    }
+    if (live) st_nt16(y + (t * H + h0 + g) * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+  }
 }
 
 }  // namespace hn
@@ -602,6 +634,31 @@ extern "C" int hn_dequantize_rows(const int8_t* q, int64_t ldq, const float* s, 
   return HN_LAUNCH_CHECK("dequant_rows_kernel");
 }
 
+template <int W, bool ROPE>
+static void qk_norm_rope_launch_g(int g, dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx, const float* w,
+                                  const float* cs, const float* sn, int64_t n_groups, int64_t H, int64_t L,
+                                  float eps, uint16_t* y) {
+  if (g == 6) hipLaunchKernelGGL((qk_norm_rope_kernel<W, ROPE, 6>), grid, dim3(256), 0, st, x, ldx, w, cs, sn, n_groups, H, L, eps, y);
+  else if (g == 4) hipLaunchKernelGGL((qk_norm_rope_kernel<W, ROPE, 4>), grid, dim3(256), 0, st, x, ldx, w, cs, sn, n_groups, H, L, eps, y);
+  else if (g == 2) hipLaunchKernelGGL((qk_norm_rope_kernel<W, ROPE, 2>), grid, dim3(256), 0, st, x, ldx, w, cs, sn, n_groups, H, L, eps, y);
+  else hipLaunchKernelGGL((qk_norm_rope_kernel<W, ROPE, 1>), grid, dim3(256), 0, st, x, ldx, w, cs, sn, n_groups, H, L, eps, y);
+}
+
+static void qk_norm_rope_launch(int w, int g, bool rope, dim3 grid, hipStream_t st, const uint16_t* x, int64_t ldx,
+                                const float* wt, const float* cs, const float* sn, int64_t n_groups, int64_t H,
+                                int64_t L, float eps, uint16_t* y) {
+  if (w == 8) {
+    if (rope) qk_norm_rope_launch_g<8, true>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+    else qk_norm_rope_launch_g<8, false>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+  } else if (w == 16) {
+    if (rope) qk_norm_rope_launch_g<16, true>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+    else qk_norm_rope_launch_g<16, false>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+  } else {
+    if (rope) qk_norm_rope_launch_g<32, true>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+    else qk_norm_rope_launch_g<32, false>(g, grid, st, x, ldx, wt, cs, sn, n_groups, H, L, eps, y);
+  }
+}
+
 extern "C" int hn_qk_norm_rope(const void* x, int64_t ldx, const float* weight, const float* cos_t, const float* sin_t,
                                int64_t B, int64_t L, int64_t H, int64_t D, float eps, void* y, void* stream) {
   HN_REQUIRE(B >= 0 && L >= 0 && H > 0, "hn_qk_norm_rope: bad shape");
@@ -612,17 +669,12 @@ extern "C" int hn_qk_norm_rope(const void* x, int64_t ldx, const float* weight, 
   HN_REQUIRE(aligned16(x) && aligned16(y), "hn_qk_norm_rope: x and y must be 16-byte aligned");
   const int64_t n_heads = B * L * H;
   if (n_heads == 0) return HN_OK;
-  const int64_t w = D / 8;
-  const unsigned blocks = (unsigned)((n_heads * w + 255) / 256);
-  hipStream_t st = (hipStream_t)stream;
-#define HN_QK(WW, R)                                                                                          \
-  hipLaunchKernelGGL((qk_norm_rope_kernel<WW, R>), dim3(blocks), dim3(256), 0, st, (const uint16_t*)x, ldx,   \
-                     weight, cos_t, sin_t, n_heads, H, L, eps, (uint16_t*)y)
-  const bool rope = cos_t != nullptr;
-  if (w == 8) { if (rope) HN_QK(8, true); else HN_QK(8, false); }
-  else if (w == 16) { if (rope) HN_QK(16, true); else HN_QK(16, false); }
-  else { if (rope) HN_QK(32, true); else HN_QK(32, false); }
-#undef HN_QK
+  const int g = H % 6 == 0 ? 6 : H % 4 == 0 ? 4 : H % 2 == 0 ? 2 : 1;
+  const int w = (int)(D / 8);
+  const int64_t n_groups = n_heads / g;
+  const unsigned blocks = (unsigned)((n_groups * w + 255) / 256);
+  qk_norm_rope_launch(w, g, cos_t != nullptr, dim3(blocks), (hipStream_t)stream, (const uint16_t*)x, ldx, weight,
+                      cos_t, sin_t, n_groups, H, L, eps, (uint16_t*)y);
   return HN_LAUNCH_CHECK("qk_norm_rope_kernel");
 }
 
@@ -636,8 +688,17 @@ extern "C" int hn_pixelumm_qk(const void* x, int64_t ldx, const void* weight_t, 
   HN_REQUIRE(aligned16(x) && aligned16(y), "hn_pixelumm_qk: x and y must be 16-byte aligned");
   const int64_t n_heads = N * H;
   if (n_heads == 0) return HN_OK;
-  const unsigned blocks = (unsigned)((n_heads * 16 + 255) / 256);
-  hipLaunchKernelGGL(pixelumm_qk_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x, ldx,
-                     (const float*)weight_t, (const float*)weight_hw, cos_t, sin_t, n_heads, H, eps, (uint16_t*)y);
+  const int g = H % 6 == 0 ? 6 : H % 4 == 0 ? 4 : H % 2 == 0 ? 2 : 1;
+  const int64_t n_groups = n_heads / g;
+  const dim3 grid((unsigned)((n_groups * 16 + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  const float* wt = (const float*)weight_t;
+  const float* whw = (const float*)weight_hw;
+  const uint16_t* xx = (const uint16_t*)x;
+  uint16_t* yy = (uint16_t*)y;
+  if (g == 6) hipLaunchKernelGGL(pixelumm_qk_kernel<6>, grid, dim3(256), 0, st, xx, ldx, wt, whw, cos_t, sin_t, n_groups, H, eps, yy);
+  else if (g == 4) hipLaunchKernelGGL(pixelumm_qk_kernel<4>, grid, dim3(256), 0, st, xx, ldx, wt, whw, cos_t, sin_t, n_groups, H, eps, yy);
+  else if (g == 2) hipLaunchKernelGGL(pixelumm_qk_kernel<2>, grid, dim3(256), 0, st, xx, ldx, wt, whw, cos_t, sin_t, n_groups, H, eps, yy);
+  else hipLaunchKernelGGL(pixelumm_qk_kernel<1>, grid, dim3(256), 0, st, xx, ldx, wt, whw, cos_t, sin_t, n_groups, H, eps, yy);
   return HN_LAUNCH_CHECK("pixelumm_qk_kernel");
 }

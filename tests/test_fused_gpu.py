@@ -181,3 +181,48 @@ def test_gated_residual_frames_matches_two_torch_ops(dev, dtype, b, t, p, d, fra
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
     with pytest.raises(RuntimeError):
         fused.gated_residual_frames(x, y, gate, frame[:, :1].expand(frame_b, t + 1, d)[:, : t + 1])
+
+
+@pytest.mark.parametrize("h", [1, 2, 3, 4, 5, 6, 12, 24])
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_qk_norm_rope_head_groups(dev, h, d):
+    """Each group of lanes normalizes G heads of one token (G = 6, 4, 2 or 1 by the head count): every head
+    of a multi-head call equals a one-head call on that head's strided view (always G = 1) bit for bit, and
+    the whole agrees with the oracle."""
+    from hy_nomas import fused
+
+    print(f"qk_norm_rope head groups h={h} d={d}", flush=True)
+    b, l = 2, 37
+    g = seeded(100 + h * 7 + d)
+    x = bf(torch.randn(b, l, h, d, generator=g) * 3)
+    w = bf(torch.rand(d, generator=g) + 0.5)
+    ang = torch.rand(l, d, generator=g) * 6.28
+    rope = (ang.cos(), ang.sin())
+    xd, wd, rd = x.to(dev), w.to(dev), (rope[0].to(dev), rope[1].to(dev))
+    for r, rdv in ((None, None), (rope, rd)):
+        got = fused.qk_norm_rope(xd, wd, rdv)
+        for k in range(h):
+            assert torch.equal(got[:, :, k:k + 1], fused.qk_norm_rope(xd[:, :, k:k + 1], wd, rdv))
+        ora = bf(torch.from_numpy(oracle.qk_norm_rope(x, w, r)))
+        assert (got.cpu() != ora).float().mean().item() < 1e-2
+
+
+@pytest.mark.parametrize("h", [1, 2, 3, 6, 24])
+def test_pixelumm_qk_head_groups(dev, h):
+    """The PixelUMM kernel's head groups: each head of a multi-head call equals a one-head call bit for bit."""
+    from hy_nomas import fused
+
+    print(f"pixelumm_qk head groups h={h}", flush=True)
+    n, d = 53, 128
+    g = seeded(200 + h)
+    x = bf(torch.randn(1, n, h, d, generator=g) * 3)
+    wt = bf(torch.rand(d // 2, generator=g) + 0.5)
+    whw = bf(torch.rand(d // 2, generator=g) + 0.5)
+    ang = torch.rand(n, d, generator=g) * 6.28
+    cos, sin = ang.cos().to(dev), ang.sin().to(dev)
+    xd, wtd, whwd = x.to(dev), wt.to(dev), whw.to(dev)
+    got = fused.pixelumm_qk(xd, wtd, whwd, cos, sin)
+    for k in range(h):
+        assert torch.equal(got[:, :, k:k + 1], fused.pixelumm_qk(xd[:, :, k:k + 1], wtd, whwd, cos, sin))
+    ref = bf(torch.from_numpy(oracle.pixelumm_qk(x, wt, whw, cos.cpu(), sin.cpu())))
+    assert (got.cpu() != ref).float().mean().item() < 1e-2
