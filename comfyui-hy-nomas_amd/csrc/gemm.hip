@@ -7,6 +7,9 @@
 
 namespace hn {
 
+// int8 codes lie in [-128, 127], so a whole-K int32 dot product is exact for K < 2^17.
+constexpr int64_t kWholeKInt32Limit = 131072;
+
 // ---------------------------------------------------------------------------------------------
 // configurations
 
@@ -132,6 +135,10 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   HN_REQUIRE(kind == HN_KIND_INT8 || kind == HN_KIND_FP8, "hn_block_gemm: bad kind %d", kind);
   HN_REQUIRE(epilogue >= HN_EPI_NONE && epilogue <= HN_EPI_SWIGLU_QUANT, "hn_block_gemm: bad epilogue %d", epilogue);
   HN_REQUIRE(epilogue != HN_EPI_ACC32 || kind == HN_KIND_INT8, "hn_block_gemm: ACC32 is int8 only");
+  // whole-K int8 accumulation holds the exact dot product in int32: |sum| <= 128 * 128 * K < 2^31
+  HN_REQUIRE(kind != HN_KIND_INT8 || (group != K && epilogue != HN_EPI_ACC32) || K < kWholeKInt32Limit,
+             "hn_block_gemm: int8 with one scale group over K=%lld would overflow the int32 accumulator "
+             "(K < %lld; use group 128)", (long long)K, (long long)kWholeKInt32Limit);
   HN_REQUIRE(epilogue != HN_EPI_GELU_QUANT || (N % 128 == 0 && qs != nullptr && ldqs >= N / 128),
              "hn_block_gemm: gelu_quant needs N %% 128 == 0 and qs [M, N/128]");
   HN_REQUIRE(out_dtype >= HN_DTYPE_BF16 && out_dtype <= HN_DTYPE_F32, "hn_block_gemm: bad out dtype %d", out_dtype);
@@ -191,6 +198,9 @@ extern "C" int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_
   HN_REQUIRE(group == 128 || group == K, "hn_qkv_heads: group must be 128 or K (got %lld)", (long long)group);
   HN_REQUIRE(kind == HN_KIND_INT8 || kind == HN_KIND_FP8, "hn_qkv_heads: bad kind %d", kind);
   HN_REQUIRE(sw_rows == 1 || (sw_rows == 128 && group == 128), "hn_qkv_heads: sw_rows must be 1, or 128 with group 128");
+  HN_REQUIRE(kind != HN_KIND_INT8 || group != K || K < kWholeKInt32Limit,
+             "hn_qkv_heads: int8 with one scale group over K=%lld would overflow the int32 accumulator (K < %lld)",
+             (long long)K, (long long)kWholeKInt32Limit);
   HN_REQUIRE(l_offset >= 0 && L_total >= l_offset + L, "hn_qkv_heads: tokens [%lld, %lld) exceed L_total=%lld",
              (long long)l_offset, (long long)(l_offset + L), (long long)L_total);
   HN_REQUIRE(B * L < ((int64_t)1 << 31), "hn_qkv_heads: B * L must be below 2^31");

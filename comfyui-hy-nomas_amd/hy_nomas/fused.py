@@ -45,6 +45,8 @@ def qk_norm_rope(x, weight, rope=None, eps=1e-6):
     """x [B, L, H, D] bf16 (rows may be strided, heads contiguous), weight [D] -> RMSNorm(x) * weight, then
     RoPE with (cos, sin) [L, D] fp32 when given.  Returns a contiguous [B, L, H, D] bf16 tensor
     (hy_nomas/fused.py:94-105)."""
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError(f"qk_norm_rope: x must be bfloat16 (the projection output), got {x.dtype}")
     _lib.require_device(x, weight)
     b, l, h, d = x.shape
     if weight.numel() != d:
@@ -113,6 +115,8 @@ def gated_residual_frames(x, y, gate, frame):
 def pixelumm_qk(x, weight_t, weight_hw, cos, sin, eps=1e-6):
     """x [1, N, H, D] (a projection's output, heads contiguous), cos/sin [N, D] fp32 -> bf16 [1, N, H, D]
     (hy_nomas/fused.py:178-186)."""
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError(f"pixelumm_qk: x must be bfloat16 (the projection output), got {x.dtype}")
     _lib.require_device(x, weight_t, weight_hw, cos, sin)
     b, n, h, d = x.shape
     if b != 1:

@@ -11,12 +11,45 @@ The group is 128 channels (the reference's layout: scales [rows, K / 128]).  A s
 column selects one scale per token (activations) or per output channel (weights); the GEMM then
 accumulates the whole K in int32 and dequantizes once.  Weights are used as stored.
 """
+import weakref
+
 import torch
 
 from . import _lib
 
 GROUP = 128
 EPILOGUES = {None: 0, "gelu": 1, "gelu_quant": 2, "swiglu_quant": 4}
+# int8 whole-K accumulation keeps the exact dot product in int32: |sum| <= 128 * 128 * K < 2^31 needs
+# K < 131072.  Longer K takes the per-group fold with the single scale repeated per group.
+WHOLE_K_INT32_LIMIT = 131072
+
+# Scale tensors already known to be positive and finite (or not), by tensor identity and in-place
+# version: {id: (weakref, version, ok)}.  The fp8 GEMM with 128 x 128 block weight scales keeps its running
+# sum in units of the current group's scale product and needs both scales positive and finite.
+_SCALES_CHECKED = {}
+
+
+def _remember_scales(t, ok):
+    key = id(t)
+    _SCALES_CHECKED[key] = (weakref.ref(t, lambda _r, key=key: _SCALES_CHECKED.pop(key, None)), t._version, ok)
+
+
+def _scales_positive_finite(t):
+    """True if every value of `t` is > 0 and finite: checked on the device once per tensor and version."""
+    hit = _SCALES_CHECKED.get(id(t))
+    if hit is not None and hit[0]() is t and hit[1] == t._version:
+        return hit[2]
+    ok = bool(torch.all((t > 0) & torch.isfinite(t)))
+    _remember_scales(t, ok)
+    return ok
+
+
+def trust_scales(*tensors):
+    """Record scale tensors made by this package's quantizers (absmax / 127 or 1, max(absmax, 1e-12) / 448,
+    clamped block scales): positive, and finite for finite inputs, so the GEMM needs no check of them."""
+    for t in tensors:
+        if t is not None:
+            _remember_scales(t, True)
 
 
 def _aligned(t, bytes_):
@@ -45,6 +78,7 @@ def quantize_activations(x, kind="int8", group=GROUP, rounding="half_away"):
     x = _rows(x)
     _lib.call("hn_quantize_act", x.data_ptr(), _lib.dtype_code(x), x.stride(0), m, k, g, _lib.KIND[kind],
               _lib.ROUND[rounding], q.data_ptr(), q.stride(0), s.data_ptr(), s.stride(0), _lib.stream(x))
+    trust_scales(s)
     return q, s
 
 
@@ -71,6 +105,28 @@ def _check_gemm(qa, sa, qw, sw, bias, kind):
         raise RuntimeError(f"block_gemm: {sw.shape[0]} weight-scale rows for {n} output channels")
     if bias is not None and (bias.dim() != 1 or bias.shape[0] != n):
         raise RuntimeError(f"block_gemm: bias of shape {tuple(bias.shape)} for {n} output channels")
+
+
+def _layout(sa, sw, n, k, kind, swiglu=False):
+    """How the GEMM reads the scales: (sw, sw_rows, group, groups).
+
+    sw_rows = 128: one weight-scale row per 128 output channels (the fp8 block layout), read as stored by
+    the per-group fold.  With fp8 codes that fold keeps its running sum in units of the current group's
+    scale product, which needs every activation and weight scale positive and finite; other scales are
+    repeated per channel instead (the reference's own layout, pixelumm.py:153), whose fold has no such
+    condition.  group = K: one scale per token and per channel, accumulated over the whole K (int8 only
+    while the int32 sum cannot overflow)."""
+    sw_rows = 1 if sw.shape[0] == n else GROUP
+    if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
+        raise RuntimeError(f"weight scales with {sw.shape[0]} rows for {n} output channels")
+    if sw_rows == GROUP and kind == "fp8" and not (_scales_positive_finite(sa) and _scales_positive_finite(sw)):
+        if swiglu:
+            raise RuntimeError("swiglu_quant: fp8 block scales must be positive and finite")
+        sw = sw.float().repeat_interleave(GROUP, dim=0)[:n]
+        sw_rows = 1
+    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1 and (kind == "fp8" or k < WHOLE_K_INT32_LIMIT):
+        return sw, sw_rows, k, 1
+    return sw, sw_rows, GROUP, k // GROUP
 
 
 def _scales(s, rows, groups):
@@ -114,15 +170,7 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
         qs = None
     if m == 0:
         return (out, qs) if quantized else out
-    # weight scales with one row per channel, or one row per 128 channels (block layout, g128 fold only)
-    sw_rows = 1 if sw.shape[0] == n else GROUP
-    if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
-        raise RuntimeError(f"weight scales with {sw.shape[0]} rows for {n} output channels")
-    # one scale per token and per channel -> whole-K accumulation; otherwise the g128 fold
-    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1:
-        group, groups = k, 1
-    else:
-        group, groups = GROUP, k // GROUP
+    sw, sw_rows, group, groups = _layout(sa, sw, n, k, kind, swiglu=mode == 4)
     sa = _scales(sa, m, groups)
     sw = _scales(sw, sw.shape[0], groups)
     qa = _rows(qa)
@@ -133,7 +181,10 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
               sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
               m, n, k, group, _lib.KIND[kind], mode, out.data_ptr(), 0 if quantized else _lib.dtype_code(out),
               out.stride(0), _lib.ptr(qs), qs.stride(0) if qs is not None else 0, _lib.stream(qa))
-    return (out, qs) if quantized else out
+    if quantized:
+        trust_scales(qs)
+        return out, qs
+    return out
 
 
 def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="int8", eps=1e-6, out=None,
@@ -163,11 +214,7 @@ def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="
         raise RuntimeError(f"qkv_heads: out must be contiguous bf16 [3, {batch}, {hidden // 128}, >= {l_offset + length}, 128]")
     if m == 0:
         return out
-    sw_rows = 1 if sw.shape[0] == n else GROUP
-    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1:
-        group, groups = k, 1
-    else:
-        group, groups = GROUP, k // GROUP
+    sw, sw_rows, group, groups = _layout(sa, sw, n, k, kind)
     sa = _scales(sa, m, groups)
     sw = _scales(sw, sw.shape[0], groups)
     qa, qw = _rows(qa), _rows(qw)
@@ -196,6 +243,8 @@ def block_gemm_acc32(qa, qw):
     n = qw.shape[0]
     if qa.dtype != torch.int8 or qw.dtype != torch.int8 or qw.shape[1] != k:
         raise RuntimeError("block_gemm_acc32: int8 codes with matching K expected")
+    if k >= WHOLE_K_INT32_LIMIT:
+        raise RuntimeError(f"block_gemm_acc32: K={k} could overflow the int32 accumulator (K < {WHOLE_K_INT32_LIMIT})")
     out = torch.empty((m, n), device=qa.device, dtype=torch.int32)
     if m == 0:
         return out

@@ -9,12 +9,25 @@ import torch
 from . import _lib, kernels
 
 
+def _quantize_rows_torch(x):
+    """Absmax per row (last dim) / 127 (1 for an all-zero row), IEEE quotient, half away from zero, clamp
+    +-127, in torch steps on x's device: the path for host tensors and head dims the device quantizer does
+    not take (multiples of 128 only)."""
+    xf = x.float()
+    peak = xf.abs().amax(dim=-1, keepdim=True)
+    scale = torch.where(peak > 0, peak / 127.0, torch.ones_like(peak))
+    y = xf / scale
+    codes = torch.trunc(y + torch.copysign(torch.full_like(y, 0.5), y)).clamp_(-127, 127)
+    return codes.to(torch.int8), scale
+
+
 def quantize_kv(x):
-    """x [L, H, D] -> (int8 [L, H, D], fp32 scale [L, H, 1]) (hy_nomas/world.py:83-90).  D % 128 == 0."""
-    _lib.require_device(x)
+    """x [L, H, D] -> (int8 [L, H, D], fp32 scale [L, H, 1]) (hy_nomas/world.py:83-90), on any device.
+    Device tensors with D % 128 == 0 take the gfx950 quantizer; host tensors and other head dims take the
+    same arithmetic in torch steps."""
     l, h, d = x.shape
-    if d % kernels.GROUP:
-        raise RuntimeError(f"quantize_kv: head dim {d} is not a multiple of {kernels.GROUP}")
+    if not x.is_cuda or d % kernels.GROUP or x.numel() == 0:
+        return _quantize_rows_torch(x)
     x2 = x.reshape(l * h, d)
     # one group per row: the g128 kernel when a row is one 128-channel group, else the per-row kernel
     q, s = kernels.quantize_activations(x2, "int8", kernels.GROUP if d == kernels.GROUP else None)
@@ -22,9 +35,11 @@ def quantize_kv(x):
 
 
 def dequantize_kv(q, scale, dtype=torch.bfloat16):
-    """(q.float() * scale).to(dtype) in one pass (hy_nomas/world.py:93-94): q [..., D] int8, scale [..., 1]."""
-    _lib.require_device(q, scale)
+    """(q.float() * scale).to(dtype) in one pass (hy_nomas/world.py:93-94): q [..., D] int8, scale [..., 1].
+    Host tensors, and head dims the device kernel does not take (D % 16 != 0), use the same torch steps."""
     d = q.shape[-1]
+    if not q.is_cuda or not scale.is_cuda or d % 16 or dtype not in _lib.DTYPE:
+        return (q.float() * scale.to(q.device)).to(dtype)
     rows = q.numel() // d if d else 0
     out = torch.empty(q.shape, device=q.device, dtype=dtype)
     if rows == 0:

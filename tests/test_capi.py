@@ -75,3 +75,9 @@ def test_argument_validation_without_a_gpu():
     assert rc == 1 and b"L_total" in l.hn_last_error()
     rc = l.hn_gated_residual_frames(None, None, None, None, 0, 1, 2, 3, 100, None, None)   # D % 8 != 0
     assert rc == 1 and b"multiple of 8" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 131072, None, 1, None, 131072, None, 1, 1, None, 0, 4, 8, 131072, 131072, 0, 0, None,
+                         0, 8, None, 0, None)   # int8 whole-K over 2^17: the int32 sum could overflow
+    assert rc == 1 and b"overflow" in l.hn_last_error()
+    rc = l.hn_block_gemm(None, 131072, None, 1024, None, 131072, None, 1024, 1, None, 0, 4, 8, 131072, 128, 0, 3,
+                         None, 0, 8, None, 0, None)   # ACC32 always sums the whole K in int32
+    assert rc == 1 and b"overflow" in l.hn_last_error()

@@ -217,6 +217,45 @@ def test_block_weight_scales(dev, kind, m, n, k):
         assert max_abs_rel(got, full) < 1e-4
 
 
+def test_fp8_block_scales_zero_and_inf(dev):
+    """fp8 codes with 128 x 128 block weight scales that are not all positive and finite: one all-zero weight
+    block at scale 0 and one all-zero activation group at scale 0 (the reference's fold multiplies them in
+    as zeros), then one infinite activation scale.  The GEMM must not turn a zero scale into NaN for the
+    whole block, as a running sum kept in units of the group's scale product would; the results follow the
+    reference's per-group fold (the oracle), which reads the block scales repeated per channel."""
+    from hy_nomas import kernels
+
+    print("fp8 block scales with zeros", flush=True)
+    m, n, k = 160, 384, 768
+    g = seeded(777)
+    x = outlier_input(m, k, seed=778)
+    qa, sa = oracle.quantize(x, 128, "fp8")
+    qa[5, 256:384] = 0
+    sa[5, 2] = 0.0
+    codes = (torch.randn(n, k, generator=g) * 100).clamp(-448, 448).to(torch.float8_e4m3fn)
+    sblk = (torch.rand(n // 128, k // 128, generator=g) * 4e-3 + 1e-3).float()
+    codes[128:256, 384:512] = 0
+    sblk[1, 3] = 0.0
+    w_codes = codes.view(torch.uint8).numpy()
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    sw_full = sblk.repeat_interleave(128, 0).contiguous()
+    qa_t = torch.from_numpy(qa).view(torch.float8_e4m3fn).to(dev)
+    got = kernels.block_gemm(qa_t, torch.from_numpy(sa).to(dev), codes.to(dev), sblk.to(dev), bias.to(dev),
+                             torch.float32, kind="fp8").cpu().numpy()
+    ref = oracle.block_gemm(qa, sa, w_codes, sw_full.numpy(), oracle.to_f32(bias), kind="fp8")
+    assert np.isfinite(got).all()
+    assert max_abs_rel(got, ref) < 4e-3
+    # an infinite activation scale poisons its own token row only, as in the reference's fold
+    sa_inf = sa.copy()
+    sa_inf[9, 1] = np.inf
+    got = kernels.block_gemm(qa_t, torch.from_numpy(sa_inf).to(dev), codes.to(dev), sblk.to(dev), bias.to(dev),
+                             torch.float32, kind="fp8").cpu().numpy()
+    rows = [r for r in range(m) if r != 9]
+    assert np.isfinite(got[rows]).all()
+    assert max_abs_rel(got[rows], ref[rows]) < 4e-3
+    assert not np.isfinite(got[9]).all()
+
+
 def test_fp8_block_linear(dev):
     """pixelumm.fp8_block_linear (block scales read directly) against F.linear on the dequantized fp8
     weights in fp32 (hy_nomas/pixelumm.py:147-155)."""

@@ -161,3 +161,45 @@ def test_fused_gate(monkeypatch):
     if torch.cuda.is_available():
         assert fused.available(torch.zeros(2, dtype=torch.bfloat16, device="cuda"))
         assert not fused.available(torch.zeros(2, dtype=torch.float16, device="cuda"))
+
+
+def test_kv_host_path_and_odd_head_dims():
+    """quantize_kv / dequantize_kv on host tensors and on head dims that are not multiples of 128 take the
+    reference's torch steps (hy_nomas/world.py:83-94): codes and scales equal the oracle's."""
+    from hy_nomas import kv
+
+    g = seeded(31)
+    for shape in ((50, 3, 128), (7, 2, 96), (5, 1, 200)):
+        x = torch.randn(*shape, generator=g).to(torch.bfloat16)
+        x[0, 0] = 0  # an all-zero (token, head) row: scale 1, codes 0
+        x[1, 0, 3] = 0.5 * x[1, 0].abs().max()   # half of the peak: an exact .5 tie of x / scale
+        q, s = kv.quantize_kv(x)
+        q_ref, s_ref = oracle.quantize_kv(x)
+        assert q.dtype == torch.int8 and s.shape == shape[:2] + (1,)
+        assert np.array_equal(q.numpy(), q_ref) and np.array_equal(s.numpy(), s_ref)
+        back = kv.dequantize_kv(q, s)
+        assert torch.equal(back, torch.from_numpy(oracle.dequantize_kv(q_ref, s_ref)))
+
+
+def test_qk_kernels_reject_other_dtypes():
+    """The QK kernels read bf16 bits: fp16 / fp32 inputs raise instead of being read as bf16."""
+    from hy_nomas import fused
+
+    x = torch.randn(1, 4, 2, 128)
+    w = torch.ones(128)
+    for dtype in (torch.float32, torch.float16):
+        with pytest.raises(RuntimeError, match="bfloat16"):
+            fused.qk_norm_rope(x.to(dtype), w)
+        with pytest.raises(RuntimeError, match="bfloat16"):
+            fused.pixelumm_qk(x.to(dtype), w[:64], w[:64], torch.ones(4, 128), torch.zeros(4, 128))
+
+
+def test_whole_k_int8_routes_long_k_to_the_group_fold(monkeypatch):
+    """A per-token x per-channel int8 GEMM with K >= 2^17 would overflow a whole-K int32 sum: the wrapper
+    hands it to the per-group fold instead (scales repeated per group); shorter K keeps whole-K mode."""
+    from hy_nomas import kernels
+
+    sa, sw = torch.ones(4, 1), torch.ones(8, 1)
+    assert kernels._layout(sa, sw, 8, 3072, "int8")[2:] == (3072, 1)
+    assert kernels._layout(sa, sw, 8, 131072, "int8")[2:] == (128, 1024)
+    assert kernels._layout(sa, sw, 8, 131072, "fp8")[2:] == (131072, 1)
