@@ -311,6 +311,13 @@ def elementwise(dev, gen, steps, warmup):
     return out
 
 
+def rope_tables(length, head_dim, gen, dev):
+    """cos / sin [length, head_dim] fp32 of random angles, each repeated for its interleaved pair (the shape
+    and layout of the model's 3-D RoPE tables; the values do not change the work)."""
+    ang = torch.rand(length, head_dim // 2, generator=gen, device=dev) * 6.283
+    return ang.cos().repeat_interleave(2, dim=1), ang.sin().repeat_interleave(2, dim=1)
+
+
 def dit_block(dev, gen, steps, warmup, per_token):
     """One synthetic double-stream DiT block forward (hy_nomas/model.py:230-286) at hidden 3072, 24 heads x 128,
     FFN 12288 GELU-tanh: 57344 image tokens (RoPE grid 14 x 64 x 64) + 256 text tokens, random int8 weights,
@@ -337,27 +344,217 @@ def dit_block(dev, gen, steps, warmup, per_token):
     txt = torch.randn(1, lt, d, generator=gen, device=dev).to(torch.bfloat16)
     mods = [[(torch.randn(1, d, generator=gen, device=dev) * 0.1).to(torch.bfloat16) for _ in range(6)]
             for _ in range(2)]
-    rope = block.rope_freqs([16, 56, 56], 256, 14, 64, 64, device=dev)
+    rope = rope_tables(lv, d // heads, gen, dev)
     with torch.no_grad():
         ms, _ = time_launches([lambda: blk.forward(img, txt, mods[0], mods[1], rope)], steps, warmup)
-        q, k, v = (torch.randn(1, lv + lt, heads, d // heads, generator=gen, device=dev).to(torch.bfloat16)
-                   for _ in range(3))
-        att_ms, _ = time_launches([lambda: block.attention(q, k, v)], steps, warmup)
+        # the block's attention call on the same operands: head-major q, k, v [B, H, L, D] as the QKV
+        # epilogue writes them (no layout copies), image and text tokens together
+        hm = torch.randn(3, 1, heads, lv + lt, d // heads, generator=gen, device=dev).to(torch.bfloat16)
+        att_ms, _ = time_launches([lambda: block.attention_heads(hm[0], hm[1], hm[2])], steps, warmup)
     ops = 2 * (lv + lt) * sum(n * k for _, k, n in STACK)
     lin_ms = ms - att_ms
-    del blk, img, txt, q, k, v
+    del blk, img, txt, hm
     torch.cuda.empty_cache()
     return {"block_ms": round(ms, 3), "attention_ms": round(att_ms, 3), "linear_path_ms": round(lin_ms, 3),
             "linear_ops": ops, "linear_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
             "activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
 
 
+# the linears of the reference's own kernel benchmark (dev/bench_kernels.py:27-28): the released checkpoint's
+# hidden 2048 / FFN 8192 DiT at 26400 tokens, the PixelUMM decoder's 4096 <-> 12288 MLP at 35200, and an M=300
+# text-length case; weights N(0, 0.02) in Tencent's g128 int8 layout, activations N(0, 2)
+REF_SHAPES = [(26400, 2048, 2048), (26400, 2048, 8192), (26400, 8192, 2048), (35200, 4096, 12288),
+              (35200, 12288, 4096), (300, 2048, 12288)]
+
+
+def reference_shapes(dev, gen, steps, warmup):
+    """Per launch at each of the reference benchmark's shapes: our int8_g128_linear (g128 activation
+    quantization + GEMM, the reference's call), the GEMM alone on pre-quantized activations, the fp8 block
+    linear (block scales read as stored, and expanded per channel as the reference passes them), and
+    torch's bf16 F.linear on the dequantized weight (hipBLASLt), with the relative error of the int8 path
+    against that bf16 product (the reference script's figure)."""
+    from hy_nomas import kernels, ops, pixelumm
+
+    F = torch.nn.functional
+    rows = []
+    for m, k, n in REF_SHAPES:
+        x = (torch.randn(m, k, generator=gen, device=dev) * 2).to(torch.bfloat16)
+        w = torch.randn(n, k, generator=gen, device=dev) * 0.02
+        bias = torch.randn(n, generator=gen, device=dev).to(torch.bfloat16)
+        q, sc = ops.quantize_g128(w)
+        wd = ops.dequantize_g128(q, sc)
+        qf, sf = pixelumm.quantize_fp8_block(w)
+        sfx = sf.repeat_interleave(128, 0).contiguous()
+        del w
+        ref = F.linear(x, wd, bias).float()
+        err = ((kernels.int8_g128_linear(x, q, sc, bias).float() - ref).norm() / ref.norm()).item()
+        err8 = ((pixelumm.fp8_block_linear(x, qf, sf, bias).float() - ref).norm() / ref.norm()).item()
+        del ref
+        qa, sa = kernels.quantize_activations(x)
+        fns = [lambda: kernels.int8_g128_linear(x, q, sc, bias),
+               lambda: kernels.block_gemm(qa, sa, q, sc, bias),
+               lambda: pixelumm.fp8_block_linear(x, qf, sf, bias),
+               lambda: kernels.block_linear(x, qf, sfx, bias, kind="fp8"),
+               lambda: F.linear(x, wd, bias)]
+        _, per = time_launches(fns, steps, warmup, 0.3)
+        ops_ = 2 * m * n * k
+        row = {"M": m, "K": k, "N": n, "int8_rel_err_vs_bf16": float(f"{err:.3e}"),
+               "fp8_rel_err_vs_bf16": float(f"{err8:.3e}")}
+        for name, t, peak in (("int8_g128_linear", per[0], PEAK_INT8_TOPS), ("int8_g128_gemm", per[1], PEAK_INT8_TOPS),
+                              ("fp8_block_linear", per[2], PEAK_FP8_TFLOPS),
+                              ("fp8_linear_expanded_scales", per[3], PEAK_FP8_TFLOPS),
+                              ("bf16_F_linear_hipblaslt", per[4], 2500.0)):
+            tops = ops_ / (t * 1e-3) / 1e12
+            row[name] = {"ms": round(t, 4), "TOPS": round(tops, 1), "frac_peak": round(tops / peak, 3)}
+        rows.append(row)
+        del x, q, sc, wd, qf, sf, sfx, qa, sa, bias, fns
+        torch.cuda.empty_cache()
+    return rows
+
+
+def peaks(dev, gen):
+    """The roofline denominators measured on this GPU with the committed probes (csrc/probes/peak.hip):
+    int8 and fp8 MFMA loops on real operand data (activation-like codes x weight codes; the power limit,
+    and with it the clock, depends on the data), two waves per SIMD, with the shader clock they ran at; and
+    a streaming 1 GiB device copy.  The roofline fraction stays against the published peaks; these show
+    what the chip sustains."""
+    import ctypes
+
+    from hy_nomas import kernels, pixelumm
+
+    path = os.path.join(ROOT, "comfyui-hy-nomas_amd", "hy_nomas", "libhynomas_probes.so")
+    lib = ctypes.CDLL(path)
+    i64, vp, ci = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+    lib.hnp_operand_bytes.restype, lib.hnp_operand_bytes.argtypes = i64, [ci]
+    lib.hnp_ops_per_mfma.restype, lib.hnp_ops_per_mfma.argtypes = i64, [ci]
+    lib.hnp_mfma_loop.argtypes = [ci, vp, vp, ci, ci, vp, vp, vp]
+    lib.hnp_copy.argtypes = [vp, vp, i64, ci, vp]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks = 2 * cus                      # 8 waves per CU, two per SIMD (as the GEMM runs)
+    waves = blocks * lib.hnp_waves_per_block()
+    stream = torch.cuda.current_stream()
+    out = {"compute_units": cus}
+    for kind, name, peak in ((0, "int8_mfma", PEAK_INT8_TOPS), (1, "fp8_mfma", PEAK_FP8_TFLOPS)):
+        nbytes = lib.hnp_operand_bytes(kind)
+        x = outlier_activations(nbytes // 256, 256, gen, dev)
+        if kind == 0:
+            a, _ = kernels.quantize_activations(x, "int8", None)
+            b = torch.randint(-127, 128, (nbytes,), generator=gen, device=dev, dtype=torch.int8)
+        else:
+            a, _ = kernels.quantize_activations(x, "fp8", 128)
+            b, _ = pixelumm.quantize_fp8_block(torch.randn(nbytes // 256, 256, generator=gen, device=dev) * 0.02)
+        a, b = a.contiguous(), b.contiguous()
+        res = torch.empty(waves * 64, dtype=torch.int32, device=dev)
+        clk = torch.zeros(2, dtype=torch.int64, device=dev)
+        iters = 20000
+
+        def launch():
+            rc = lib.hnp_mfma_loop(kind, a.data_ptr(), b.data_ptr(), iters, blocks, res.data_ptr(), clk.data_ptr(),
+                                   stream.cuda_stream)
+            if rc:
+                raise RuntimeError(f"hnp_mfma_loop failed ({rc})")
+
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < WARM_S:
+            launch()
+            torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record(stream)
+        for _ in range(5):
+            launch()
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+        ms = ev[0].elapsed_time(ev[1]) / 5
+        ops = waves * iters * lib.hnp_mfma_per_iter() * lib.hnp_ops_per_mfma(kind)
+        cycles, ticks = clk.tolist()
+        tops = ops / (ms * 1e-3) / 1e12
+        out[name] = {"TOPS": round(tops, 1), "frac_published_peak": round(tops / peak, 3),
+                     "clock_GHz": round(cycles / (ticks / 100e6) / 1e9, 3), "ms_per_launch": round(ms, 3)}
+        del a, b, x, res, clk
+    nb = 1 << 30
+    src = torch.empty(nb, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(7)
+
+    def copy():
+        if lib.hnp_copy(src.data_ptr(), dst.data_ptr(), nb, cus * 8, stream.cuda_stream):
+            raise RuntimeError("hnp_copy failed")
+
+    for _ in range(3):
+        copy()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(stream)
+    for _ in range(10):
+        copy()
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / 10
+    gbs = 2 * nb / (ms * 1e-3) / 1e9
+    out["copy_1GiB"] = {"GB/s": round(gbs, 1), "frac_published_peak": round(gbs / PEAK_HBM_GBS, 3),
+                        "ms": round(ms, 3)}
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
+def config0_gpu(dev, steps, warmup):
+    """The CPU-baseline workload on the GPU: x bf16 [1024, 3072] ~N(0, 1) with 1 % of the channels x20,
+    per-token int8 quantization with round-half-even, per-channel int8 weights [3072, 3072] with fp32 scales
+    ~U(1e-3, 5e-3), bf16 bias, bf16 out; seed 0.  Quantization + GEMM per launch."""
+    from hy_nomas import kernels
+
+    m, k, n = 1024, HIDDEN, HIDDEN
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: k // 100]] *= 20
+    x = x.to(torch.bfloat16).to(dev)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+    sw = (torch.rand(n, 1, generator=g) * 4e-3 + 1e-3).to(dev)
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+
+    def linear():
+        qa, sa = kernels.quantize_activations(x, "int8", None, rounding="half_even")
+        return kernels.block_gemm(qa, sa, w, sw, bias)
+
+    _, per = time_launches([linear], steps, warmup, 0.3)
+    ops = 2 * m * n * k
+    return {"ms": round(per[0], 4), "TOPS": round(ops / (per[0] * 1e-3) / 1e12, 1), "ops": ops,
+            "workload": "W8A8 linear 1024x3072 -> 3072, per-token half-even int8 activations, per-channel "
+                        "int8 weights, bias, bf16 out (quantization + GEMM)"}
+
+
+def cpu_host():
+    """The host CPU: model name, logical CPUs, CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity}
+
+
+# Threads for the CPU legs: the GPU box grants one GPU's job a 16-CPU share (its worker pools and
+# OMP_NUM_THREADS are sized to it), whatever the host's CPU count.
+CPU_SHARE = 16
+
+
 def cpu_baseline(target_s=20.0):
     """The reference's CPU fallback (hy_nomas/ops.py:172-176: dequantize the g128 int8 weight to bf16, then
-    F.linear) on a row sample of the four GEMMs; rows are scaled so the timed work is ~target_s."""
+    F.linear) on a row sample of the four GEMMs; rows are scaled so the timed work is ~target_s.  Beside it,
+    the single W8A8 linear of the CPU workload (1024 x 3072 -> 3072) through the same fallback and through
+    the oracle's W8A8 restatement, and torch's elementwise forms."""
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    host = cpu_host()
+    threads = max(1, min(host["affinity_cpus"], CPU_SHARE))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     layers = []
@@ -384,14 +581,51 @@ def cpu_baseline(target_s=20.0):
     ops = sum(2 * rows * n * k for _, k, n in STACK)
     return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": f"{rows} token rows of each of the 4 GEMMs (M=32768 full), median of {reps}, "
-                      f"{dt:.2f} s per pass; dequantize_g128 + bf16 F.linear",
-            "also": cpu_restatements(threads)}
+                      f"{dt:.2f} s per pass; dequantize_g128 + bf16 F.linear (the reference's CPU fallback), "
+                      f"{threads} threads (this job's CPU share) on {host['cpu_model']}",
+            "host": host, "config0": cpu_config0(), "also": cpu_restatements(threads)}
+
+
+def cpu_config0():
+    """The single W8A8 linear of the CPU workload (x bf16 [1024, 3072] with 1 % outlier channels x20, int8
+    weights [3072, 3072] with per-channel scales, bias; seed 0), median of 10 after 3 warm-ups: the
+    reference's fallback (dequantize + bf16 F.linear; it does not quantize activations) and the oracle's W8A8
+    restatement (per-token half-even quantization, exact integer products, dequantization + bias)."""
+    import oracle
+
+    m, k, n = 1024, HIDDEN, HIDDEN
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: k // 100]] *= 20
+    x = x.to(torch.bfloat16)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = (torch.rand(n, 1, generator=g) * 4e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    wn, swn, bn = w.numpy(), sw.numpy(), oracle.to_f32(bias)
+
+    def w8a8():
+        qa, sa = oracle.quantize(x, k, "int8", rounding="half_even")
+        return oracle.block_gemm(qa, sa, wn, swn, bn)
+
+    out = {}
+    ops = 2 * m * n * k
+    for name, fn in (("reference_fallback", lambda: oracle.dequant_linear(x, w, sw, bias)), ("w8a8_oracle", w8a8)):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(10):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        t = sorted(ts)[len(ts) // 2]
+        out[name] = {"ms": round(t * 1e3, 3), "TOPS": round(ops / t / 1e12, 4)}
+    return out
 
 
 def cpu_restatements(threads):
-    """The W8A8 arithmetic of the path restated on the CPU, timed beside the fallback: the oracle's int8
-    g128 GEMM at 1024 x 3072 -> 3072 (19.3 G ops), its g128 activation quantizer, and the torch forms of
-    adaLN and the gated residual at [1, 32768, 3072] (median of 3 each)."""
+    """The arithmetic of the path restated on the CPU, timed beside the fallback: the oracle's g128
+    activation quantizer and the torch forms of adaLN and the gated residual at [1, 32768, 3072] (median of 3
+    each, one for the quantizer)."""
     import oracle
 
     g = torch.Generator().manual_seed(1)
@@ -405,12 +639,6 @@ def cpu_restatements(threads):
             ts.append(time.perf_counter() - t0)
         return sorted(ts)[reps // 2]
 
-    m, k, n = 1024, HIDDEN, HIDDEN
-    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
-    qa, sa = oracle.quantize(x)
-    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).numpy()
-    sw = (torch.rand(n, k // 128, generator=g) * 4e-3 + 1e-3).numpy()
-    t_gemm = med(lambda: oracle.block_gemm(qa, sa, w, sw))
     big = torch.randn(1, M, HIDDEN, generator=g).to(torch.bfloat16)
     y = torch.randn(1, M, HIDDEN, generator=g).to(torch.bfloat16)
     shift = (torch.randn(1, HIDDEN, generator=g) * 0.1).to(torch.bfloat16)
@@ -423,7 +651,6 @@ def cpu_restatements(threads):
     t_gr = med(lambda: big + y * gate[:, None])
     n_el = M * HIDDEN
     return {"threads": threads,
-            "w8a8_oracle_gemm_1024x3072x3072": {"s": round(t_gemm, 3), "TOPS": round(2 * m * n * k / t_gemm / 1e12, 4)},
             "quantize_g128_oracle_GBps": round(n_el * (3 + 4 / 128) / t_quant / 1e9, 2),
             "adaln_torch_GBps": round(n_el * 4 / t_adaln / 1e9, 2),
             "gated_residual_torch_GBps": round(n_el * 6 / t_gr / 1e9, 2)}
@@ -437,7 +664,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--block-only", action="store_true", help="only the DiT block forward (both layouts)")
-    ap.add_argument("--only", choices=["fp8", "g128", "elementwise"],
+    ap.add_argument("--only", choices=["fp8", "g128", "elementwise", "peaks", "refshapes", "config0"],
                     help="only one of the extra measurements (for per-kernel profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 512 MiB five times (HBM counter calibration)")
@@ -471,6 +698,15 @@ def main():
         ms_g, per_g, ops = gemm_stack(dev, gen, args.steps, args.warmup, group_mode="g128")
         print(json.dumps({"int8_g128_stack_ms": round(ms_g, 4), "per_gemm_ms": [round(t, 4) for t in per_g],
                           "TOPS": round(ops / (ms_g * 1e-3) / 1e12, 1)}))
+        return
+    if args.only == "peaks":
+        print(json.dumps({"peaks": peaks(dev, gen)}))
+        return
+    if args.only == "refshapes":
+        print(json.dumps({"reference_shapes": reference_shapes(dev, gen, max(5, args.steps // 2), 2)}))
+        return
+    if args.only == "config0":
+        print(json.dumps({"config0_gpu": config0_gpu(dev, args.steps, args.warmup)}))
         return
     if args.only == "elementwise":
         print(json.dumps(elementwise(dev, gen, max(10, args.steps), 3)))
@@ -549,10 +785,22 @@ def main():
                 extra[name] = dit_block(dev, gen, 3, 1, pt)
             except RuntimeError as e:  # e.g. no flash / memory-efficient SDPA kernel for this device
                 extra[name] = {"error": str(e)[:200]}
+        log("bench: the reference benchmark's shapes (g128 int8, fp8 blocks, bf16)")
+        extra["reference_shapes"] = reference_shapes(dev, gen, max(5, args.steps // 2), 2)
+        log("bench: peak probes")
+        extra["peaks"] = peaks(dev, gen)
+        result["roofline"]["measured_ceiling"] = {
+            "int8_mfma_TOPS": extra["peaks"]["int8_mfma"]["TOPS"],
+            "frac_of_measured": round(achieved / extra["peaks"]["int8_mfma"]["TOPS"], 3),
+            "note": "MFMA loop on real operand data at the power-limited clock (extra.peaks); frac stays "
+                    "against the published peak"}
         result["extra"] = extra
     if not args.no_cpu:
+        log("bench: config 0 on the GPU")
+        gpu0 = config0_gpu(dev, args.steps, args.warmup)
         log("bench: cpu baseline")
         result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"]["config0"]["gpu"] = gpu0
     print(json.dumps(result), flush=True)
 
 

@@ -16,6 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "hy_nomas", "libhynomas_hip.so")
+# the benchmark's peak-rate probes (csrc/probes/): a library of their own, not part of the C ABI
+PROBES_OUT = os.path.join(HERE, "hy_nomas", "libhynomas_probes.so")
 ARCH = "gfx950"
 
 # -ffp-contract=off: every fused multiply-add in the kernels is written explicitly.
@@ -33,12 +35,14 @@ def hipcc():
 
 def build(verbose=False, jobs=None):
     os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    libs = {OUT: sorted(glob.glob(os.path.join(CSRC, "*.hip"))),
+            PROBES_OUT: sorted(glob.glob(os.path.join(CSRC, "probes", "*.hip")))}
+    sources = [src for srcs in libs.values() for src in srcs]
     jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
-    objects, running = [], []
+    objects, running = {}, []
     for src in sources:
-        obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-        objects.append(obj)
+        obj = os.path.join(BUILD, os.path.relpath(src, CSRC).replace(os.sep, "_") + ".o")
+        objects[src] = obj
         cmd = [hipcc()] + HIPCC_FLAGS + ["-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -47,12 +51,13 @@ def build(verbose=False, jobs=None):
             _reap(running.pop(0), verbose)
     while running:
         _reap(running.pop(0), verbose)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"] + objects + ["-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
-    os.replace(tmp, OUT)
+    for out, srcs in libs.items():
+        tmp = out + ".tmp"
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC"] + [objects[s] for s in srcs] + ["-o", tmp]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, out)
     return OUT
 
 

@@ -1,7 +1,4 @@
-"""The DiT double-stream block half on the quantized path, and the torch helpers it is checked against.
-
-Helpers (hy_nomas/model.py:89-138): `layer_norm`, `modulate`, `RMSNorm`, `rope_freqs`, `apply_rope` -- the
-torch arithmetic the fused kernels replace.
+"""The DiT double-stream block on the quantized path.
 
 `DiTBlockInt8` wires one stream of `DoubleStreamBlock` (hy_nomas/model.py:246-286) through this package's
 kernels: fused LayerNorm/modulate/int8 quantization -> int8 QKV GEMM (q, k, v weights concatenated along
@@ -13,54 +10,6 @@ import torch
 import torch.nn.functional as F
 
 from . import fused, kernels
-
-
-def layer_norm(x, eps=1e-6):
-    """LayerNorm without affine in fp32 (hy_nomas/model.py:103-106)."""
-    return F.layer_norm(x.float(), (x.shape[-1],), eps=eps)
-
-
-def modulate(x, shift, scale):
-    """hy_nomas/model.py:109-111 (fp32 when x is an fp32 norm)."""
-    return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
-
-
-class RMSNorm(torch.nn.Module):
-    """Normalize in fp32, cast back, then scale in the input dtype (hy_nomas/model.py:89-100)."""
-
-    def __init__(self, dim, eps=1e-6, dtype=None, device=None):
-        super().__init__()
-        self.eps = eps
-        self.weight = torch.nn.Parameter(torch.ones(dim, dtype=dtype, device=device))
-
-    def forward(self, x):
-        out = x.float()
-        out = (out * torch.rsqrt(out.pow(2).mean(-1, keepdim=True) + self.eps)).type_as(x)
-        return out * self.weight.to(dtype=out.dtype, device=out.device)
-
-
-def rope_freqs(rope_dims, theta, t, h, w, t_offset=0, device=None):
-    """3-D RoPE tables (cos, sin) [t*h*w, sum(rope_dims)] on the grid [t_offset, t_offset + t) x [0, h) x [0, w),
-    fp32, each angle repeated for its interleaved pair (hy_nomas/model.py:114-128)."""
-    axes = []
-    for start, n in ((t_offset, t), (0, h), (0, w)):
-        axes.append(torch.linspace(start, start + n, n + 1, dtype=torch.float32, device=device)[:n])
-    grid = torch.meshgrid(*axes, indexing="ij")
-    cos, sin = [], []
-    for dim, pos in zip(rope_dims, grid):
-        freqs = 1.0 / (theta ** (torch.arange(0, dim, 2, device=device)[: dim // 2].float() / dim))
-        angles = torch.outer(pos.reshape(-1), freqs)
-        cos.append(angles.cos().repeat_interleave(2, dim=1))
-        sin.append(angles.sin().repeat_interleave(2, dim=1))
-    return torch.cat(cos, dim=1), torch.cat(sin, dim=1)
-
-
-def apply_rope(x, cos, sin):
-    """Interleaved-pair rotation in fp32, cast back (hy_nomas/model.py:131-138).  x [B, L, H, D]."""
-    xf = x.float()
-    real, imag = xf.reshape(*x.shape[:-1], -1, 2).unbind(-1)
-    rotated = torch.stack([-imag, real], dim=-1).flatten(3)
-    return (xf * cos[None, :, None, :] + rotated * sin[None, :, None, :]).type_as(x)
 
 
 class Int8Linear:
@@ -93,17 +42,6 @@ class DiTBlockInt8:
         self.per_token = per_token
         self.group = None if per_token else kernels.GROUP
 
-    def attention_inputs(self, x, shift1, scale1, rope=None):
-        """adaLN + int8 quantization shared by q/k/v -> one QKV GEMM -> QK-norm (+RoPE).  x [B, L, D]."""
-        b, n, d = x.shape
-        qa, sa = kernels.adaln_quant(x, shift1, scale1, group=self.group)
-        qkv = kernels.block_gemm(qa, sa, self.qkv.qw, self.qkv.sw, self.qkv.bias, out_dtype=x.dtype)
-        qkv = qkv.view(b, n, 3, self.heads, d // self.heads)
-        q = fused.qk_norm_rope(qkv[:, :, 0], self.q_norm_w, rope)
-        k = fused.qk_norm_rope(qkv[:, :, 1], self.k_norm_w, rope)
-        v = qkv[:, :, 2]
-        return q, k, v
-
     def attention_heads(self, x, shift1, scale1, rope=None, out=None, l_offset=0):
         """adaLN + int8 quantization -> one QKV GEMM whose epilogue applies QK-norm (+RoPE) and writes q, k, v
         head-major: out [3, B, H, L_total, D] (tokens at l_offset ..).  x [B, L, D]."""
@@ -131,20 +69,6 @@ class DiTBlockInt8:
         hm = self.attention_heads(x, shift1, scale1, rope)
         attn = attention_heads(hm[0], hm[1], hm[2]).reshape(x.shape)
         return self.post(x, attn, gate1, shift2, scale2, gate2)
-
-
-def attention(q, k, v):
-    """Joint softmax attention over the token axis with torch SDPA: q, k, v [B, L, H, D] -> [B, L, H, D].
-
-    The operands are made contiguous in [B, H, L, D] first (torch's batched bf16 products misbehave on
-    transposed views), and only the flash / memory-efficient kernels are allowed: at video lengths the
-    math fallback would materialize an [L, L] score matrix per head, so an unsupported case raises."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-
-    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-        out = F.scaled_dot_product_attention(qh, kh, vh)
-    return out.transpose(1, 2)
 
 
 def attention_heads(qh, kh, vh):
@@ -183,42 +107,3 @@ class DoubleStreamBlockInt8:
         img = self.img.post(img, attn[:, :lv], gate1, shift2, scale2, gate2)
         txt = self.txt.post(txt, attn[:, lv:], tgate1, tshift2, tscale2, tgate2)
         return img, txt
-
-
-def reference_double_stream(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope=None, eps=1e-6):
-    """The same double-stream block in float32 torch arithmetic with dequantized weights and unquantized
-    activations (the reference's exact-matmul path, hy_nomas/model.py:246-286 with ops.py:172-176); tensors may
-    live on any device.  Returns (img, txt) float32."""
-    def lin(x, l):
-        w = l.qw.float() * l.sw.float().repeat_interleave(l.qw.shape[1] // l.sw.shape[1], dim=1)
-        return F.linear(x, w, None if l.bias is None else l.bias.float())
-
-    def qkv(blk, x, mods, rope):
-        shift1, scale1 = mods[0].float(), mods[1].float()
-        xm = modulate(layer_norm(x, eps), shift1, scale1).to(torch.bfloat16).float()
-        b, n, d = x.shape
-        t = lin(xm, blk.qkv).view(b, n, 3, blk.heads, d // blk.heads)
-        q, k, v = t[:, :, 0], t[:, :, 1], t[:, :, 2]
-
-        def rms(z, w):
-            return z * torch.rsqrt(z.pow(2).mean(-1, keepdim=True) + eps) * w.float()
-        q, k = rms(q, blk.q_norm_w), rms(k, blk.k_norm_w)
-        if rope is not None:
-            q, k = apply_rope(q, *rope), apply_rope(k, *rope)
-        return q, k, v
-
-    def post(blk, x, attn, mods):
-        gate1, shift2, scale2, gate2 = (m.float() for m in mods[2:])
-        x = x + lin(attn, blk.proj) * gate1.unsqueeze(1)
-        h = lin(modulate(layer_norm(x, eps), shift2, scale2), blk.fc1)
-        h = F.gelu(h, approximate="tanh")
-        return x + lin(h, blk.fc2) * gate2.unsqueeze(1)
-
-    img, txt = img.float(), txt.float()
-    iq, ik, iv = qkv(img_blk, img, img_mods, rope)
-    tq, tk, tv = qkv(txt_blk, txt, txt_mods, None)
-    q, k, v = (torch.cat(p, dim=1).transpose(1, 2) for p in ((iq, tq), (ik, tk), (iv, tv)))
-    att = torch.softmax(q @ k.transpose(-1, -2) / q.shape[-1] ** 0.5, dim=-1) @ v
-    att = att.transpose(1, 2).reshape(img.shape[0], -1, img.shape[2])
-    lv = img.shape[1]
-    return post(img_blk, img, att[:, :lv], img_mods), post(txt_blk, txt, att[:, lv:], txt_mods)

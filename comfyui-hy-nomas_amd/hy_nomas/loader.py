@@ -1,90 +1,142 @@
-"""Hy-Nomas DiT checkpoints -> the int8 linear path (hy_nomas/loader.py:25-115).
+"""Hy-Nomas DiT checkpoints -> the int8 linear path (the reference's hy_nomas/loader.py:25-115).
 
-Files are detected from their tensors, as the reference does:
-* Tencent's INT8 file (`nomas-int8-bf16-single-v1`): `weight_q` int8 [N, K] + `weight_scale` fp32 [N, K/128] per
-  Linear, everything else bf16.  Used as stored.
-* a float file with plain `weight` tensors: cast to bf16, or quantized at load to the same int8 layout.
+The on-disk formats, as the reference's loader accepts them:
 
-Files are read with safetensors (no code runs from a file).  The reference builds a ComfyUI MODEL from the state
-dict; without ComfyUI this module builds the double-stream blocks of `block.py` instead, so a checkpoint's
-weights run on the HIP GEMMs directly.
+* Tencent's int8 release, metadata ``format = nomas-int8-bf16-single-v1``: every quantized Linear stores
+  ``<name>.weight_q`` (int8 [N, K]) and ``<name>.weight_scale`` (fp32 [N, ceil(K / 128)], one scale per
+  output channel and 128 input channels); all other tensors are bf16.  It is used as stored.
+* float releases (fp32 or bf16 ``<name>.weight``), recognised by the first block's image q projection.  They
+  are cast to bf16 and may be quantized at load to the int8 layout above: every 2-D ``.weight`` whose K is a
+  multiple of 128, except the small modules the int8 release also keeps in bf16.
+
+Files are read with safetensors (tensors) and by parsing the safetensors JSON header (names and metadata); no
+code runs from a file.  Without ComfyUI this module builds the double-stream blocks of `block.py` from the
+state dict, so a checkpoint's weights run on the HIP GEMMs directly.
 """
 import json
+import struct
 
 import torch
 
 from . import ops as nomas_ops
 
+INT8_FORMAT = "nomas-int8-bf16-single-v1"
+CODES_SUFFIX, SCALES_SUFFIX = "weight_q", "weight_scale"
+# a float file holds this tensor; an int8 file holds its codes / scales instead
+FLOAT_MARKER = "double_blocks.0.img_attn_q.weight"
+# the released model's shape; the block depth and the camera flag are read from the keys
 UNET_CONFIG = {
     "in_channels": 32, "out_channels": 32, "hidden_size": 2048, "heads_num": 16, "mlp_width_ratio": 4,
     "mm_double_blocks_depth": 54, "rope_dim_list": [16, 56, 56], "rope_theta": 256, "text_states_dim": 3584,
 }
-# small modules the int8 path keeps unquantized when quantizing a float checkpoint, as Tencent's file does
+# key prefixes whose weights the int8 release stores in bf16 (patch embedding, camera and action modules)
 KEEP_FLOAT = ("action_modules.", "extrinsics_embedding_camctrl", "c2ws_hidden_states_layer", "img_in.")
-INT8_FORMAT = "nomas-int8-bf16-single-v1"
+# metadata entries a checkpoint description reports
+DESCRIPTIVE_KEYS = ("format", "model_type", "quantization", "group_size", "source_sha256")
+_HEADER_LIMIT = 1 << 28   # bytes of JSON header accepted before the file is taken as something else
+
+
+def read_header(path):
+    """(tensor table, metadata) of a safetensors file, from its header alone: an 8-byte little-endian length,
+    then that many bytes of JSON mapping tensor names to {dtype, shape, data_offsets}, with the optional
+    string map ``__metadata__``.  Raises OSError / ValueError for a file that is not one."""
+    with open(path, "rb") as handle:
+        raw = handle.read(8)
+        if len(raw) != 8:
+            raise ValueError(f"{path}: too short for a safetensors header")
+        (size,) = struct.unpack("<Q", raw)
+        if size == 0 or size > _HEADER_LIMIT:
+            raise ValueError(f"{path}: implausible safetensors header size {size}")
+        body = handle.read(size)
+    if len(body) != size:
+        raise ValueError(f"{path}: truncated safetensors header")
+    table = json.loads(body.decode("utf-8"))
+    if not isinstance(table, dict):
+        raise ValueError(f"{path}: the safetensors header is not a JSON object")
+    metadata = table.pop("__metadata__", None) or {}
+    return table, metadata
+
+
+def _block_layout(keys):
+    """(number of double blocks, has a camera module) from the state-dict keys."""
+    top = -1
+    camera = False
+    for key in keys:
+        parts = key.split(".", 2)
+        if parts[0] == "double_blocks" and len(parts) > 1 and parts[1].isdigit():
+            top = max(top, int(parts[1]))
+        elif parts[0] == "action_modules":
+            camera = True
+    return top + 1, camera
 
 
 def detect(state_dict, metadata):
-    """"int8" or "float" (hy_nomas/loader.py:34-40); anything else raises ValueError."""
-    fmt = (metadata or {}).get("format")
-    if fmt == INT8_FORMAT or any(k.endswith(".weight_q") for k in state_dict):
+    """The checkpoint kind, "int8" or "float" (the reference's loader.py:34-40); ValueError for anything that
+    is not a Hy-Nomas DiT file.  The metadata's format tag decides first, then the tensor names."""
+    if (metadata or {}).get("format") == INT8_FORMAT:
         return "int8"
-    if "double_blocks.0.img_attn_q.weight" in state_dict:
+    codes = "." + CODES_SUFFIX
+    for key in state_dict:
+        if key.endswith(codes):
+            return "int8"
+    if FLOAT_MARKER in state_dict:
         return "float"
-    raise ValueError("not a Hy-Nomas DiT checkpoint (no double_blocks.0.img_attn_q weights)")
+    raise ValueError(f"not a Hy-Nomas DiT checkpoint: no {INT8_FORMAT} code tensors and no {FLOAT_MARKER}")
 
 
 def config_from_state_dict(state_dict):
-    """The reference's UNET_CONFIG with the block depth and camera flag read from the keys (loader.py:43-48)."""
-    cfg = dict(UNET_CONFIG)
-    depth = 1 + max(int(k.split(".")[1]) for k in state_dict if k.startswith("double_blocks."))
-    cfg["mm_double_blocks_depth"] = depth
-    cfg["camera"] = any(k.startswith("action_modules.") for k in state_dict)
-    return cfg
+    """The model config for a state dict: the released shape with the block depth and the camera flag taken
+    from the keys (loader.py:43-48)."""
+    depth, camera = _block_layout(state_dict)
+    if depth == 0:
+        raise ValueError("state dict has no double_blocks.<i> tensors")
+    return {**UNET_CONFIG, "mm_double_blocks_depth": depth, "camera": camera}
+
+
+def quantizable(key, tensor):
+    """True for the weights the int8 release stores as code / scale pairs: 2-D Linear weights whose input
+    width is a multiple of 128, outside the modules kept in bf16."""
+    return (key.endswith(".weight") and tensor.ndim == 2 and tensor.shape[1] % 128 == 0
+            and not key.startswith(KEEP_FLOAT))
 
 
 def quantize_state_dict(state_dict):
-    """A float checkpoint's Linear weights -> Tencent's int8 g128 pairs (hy_nomas/loader.py:51-62).  Weights on a
-    GPU are quantized by the device kernel; CPU tensors by the reference's torch steps (`ops.quantize_g128`)."""
+    """A float state dict with every quantizable weight replaced by its int8 g128 pair (loader.py:51-62, with
+    ops.quantize_g128: the device kernel for GPU tensors, the reference's torch steps for host tensors).
+    Other tensors are passed through unchanged."""
     out = {}
-    for key, value in state_dict.items():
-        if (key.endswith(".weight") and value.ndim == 2 and not key.startswith(KEEP_FLOAT)
-                and value.shape[1] % 128 == 0):
-            q, s = nomas_ops.quantize_g128(value)
-            out[key[:-len("weight")] + "weight_q"] = q
-            out[key[:-len("weight")] + "weight_scale"] = s
+    for key, tensor in state_dict.items():
+        if quantizable(key, tensor):
+            stem = key[: -len("weight")]
+            out[stem + CODES_SUFFIX], out[stem + SCALES_SUFFIX] = nomas_ops.quantize_g128(tensor)
         else:
-            out[key] = value
+            out[key] = tensor
     return out
 
 
 def load_state_dict(path, quantize=False):
-    """(state_dict, metadata, kind) of a safetensors checkpoint (the reference's `load_dit` minus the ComfyUI
-    model): float files are cast to bf16 and, with `quantize`, turned into int8 pairs."""
-    from safetensors import safe_open
+    """(state_dict, metadata, kind) of a checkpoint file (the reference's load_dit up to the model build):
+    a float file is cast to bf16 and, with `quantize`, turned into int8 pairs (kind "int8" then)."""
     from safetensors.torch import load_file
 
-    with safe_open(path, framework="pt", device="cpu") as handle:
-        metadata = handle.metadata() or {}
+    _, metadata = read_header(path)
     state_dict = load_file(path, device="cpu")
     kind = detect(state_dict, metadata)
     if kind == "float":
-        state_dict = {k: (v.to(torch.bfloat16) if v.is_floating_point() else v) for k, v in state_dict.items()}
+        state_dict = {k: v.to(torch.bfloat16) if v.is_floating_point() else v for k, v in state_dict.items()}
         if quantize:
-            state_dict = quantize_state_dict(state_dict)
-            kind = "int8"
+            state_dict, kind = quantize_state_dict(state_dict), "int8"
     return state_dict, metadata, kind
 
 
 def _linear(state_dict, prefix, device):
     from .block import Int8Linear
 
-    try:
-        q, s = state_dict[prefix + ".weight_q"], state_dict[prefix + ".weight_scale"]
-    except KeyError:
-        raise ValueError(f"checkpoint has no int8 weight for {prefix} (quantize a float file first)") from None
+    codes, scales = state_dict.get(f"{prefix}.{CODES_SUFFIX}"), state_dict.get(f"{prefix}.{SCALES_SUFFIX}")
+    if codes is None or scales is None:
+        raise ValueError(f"checkpoint has no int8 weight for {prefix} (quantize a float file first)")
     bias = state_dict.get(prefix + ".bias")
-    return Int8Linear(q.to(device).contiguous(), s.to(device).float().contiguous(),
+    return Int8Linear(codes.to(device).contiguous(), scales.to(device).float().contiguous(),
                       None if bias is None else bias.to(device, torch.bfloat16).contiguous())
 
 
@@ -108,18 +160,16 @@ def double_block(state_dict, index, heads, device="cuda"):
 
 
 def info(metadata):
-    """The descriptive metadata keys of a checkpoint (hy_nomas/loader.py:102-106)."""
-    if not metadata:
-        return {}
-    keep = ("format", "model_type", "quantization", "group_size", "source_sha256")
-    return {k: metadata[k] for k in keep if k in metadata}
+    """The descriptive entries of a checkpoint's metadata (loader.py:102-106)."""
+    metadata = metadata or {}
+    return {key: metadata[key] for key in DESCRIPTIVE_KEYS if key in metadata}
 
 
 def describe_file(path):
-    """`info` of a file as JSON, "{}" when it cannot be read (hy_nomas/loader.py:109-115)."""
+    """`info` of a file's metadata as JSON, or "{}" when the file cannot be read as safetensors
+    (loader.py:109-115)."""
     try:
-        from safetensors import safe_open
-        with safe_open(path, framework="pt", device="cpu") as handle:
-            return json.dumps(info(handle.metadata()))
-    except Exception:
+        _, metadata = read_header(path)
+    except (OSError, ValueError):
         return "{}"
+    return json.dumps(info(metadata))

@@ -5,7 +5,6 @@ GEMM, and the checkpoint reader (the FP8 layout, dispatch, MLP and loader of the
 package).
 """
 import dataclasses
-import logging
 
 import torch
 import torch.nn.functional as F
@@ -175,21 +174,25 @@ class MLP(torch.nn.Module):
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
+DECODER_PREFIX = "decoder."
+
+
 def load_state_dict(path):
-    """`decoder.*` tensors of a PixelUMM checkpoint, prefix stripped, and whether it holds FP8 block-128
-    weights (hy_nomas/pixelumm.py:470-485).  Read with safetensors; nothing in the file executes."""
+    """(state dict, holds FP8 block-128 weights) of a PixelUMM checkpoint: its ``decoder.*`` tensors with the
+    prefix removed (the reference's pixelumm.py:470-485).  The tensor names and the metadata come from the
+    safetensors header, the tensors from safetensors; nothing in the file executes.  A file without decoder
+    tensors raises ValueError."""
     from safetensors import safe_open
 
-    state = {}
+    from .loader import read_header
+
+    table, metadata = read_header(path)
+    names = [name for name in table if name.startswith(DECODER_PREFIX)]
+    if not names:
+        raise ValueError(f"{path}: no {DECODER_PREFIX}* tensors, so not a PixelUMM checkpoint")
     with safe_open(path, framework="pt", device="cpu") as handle:
-        metadata = handle.metadata() or {}
-        for key in handle.keys():
-            if key.startswith("decoder."):
-                state[key[len("decoder."):]] = handle.get_tensor(key)
-    if not state:
-        raise ValueError(f"{path} has no decoder.* tensors: not a PixelUMM checkpoint")
-    fp8 = metadata.get("format") == FP8_FORMAT or any(k.endswith(".fp8_weight") for k in state)
-    logging.info("Hy-Nomas: PixelUMM decoder %s (%d tensors)", "FP8 block-128" if fp8 else "bf16", len(state))
+        state = {name[len(DECODER_PREFIX):]: handle.get_tensor(name) for name in names}
+    fp8 = metadata.get("format") == FP8_FORMAT or any(name.endswith(".fp8_weight") for name in state)
     return state, fp8
 
 

@@ -32,6 +32,7 @@ def make_stream(d, heads, mlp, g, per_token, dev):
 @pytest.mark.parametrize("per_token", [False, True])
 def test_double_stream_block(dev, per_token):
     from hy_nomas import block
+    from oracle import torch_forms
 
     print(f"double-stream block per_token={per_token}", flush=True)
     d, heads, mlp, lv, lt = 256, 2, 1024, 200, 40
@@ -42,12 +43,12 @@ def test_double_stream_block(dev, per_token):
     txt = torch.randn(1, lt, d, generator=g).to(torch.bfloat16)
     img_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16) for _ in range(6)]
     txt_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16) for _ in range(6)]
-    rope = block.rope_freqs([32, 48, 48], 256, 2, 10, 10)
+    rope = torch_forms.rope_freqs([32, 48, 48], 256, 2, 10, 10)
     blk = block.DoubleStreamBlockInt8(img_blk, txt_blk)
     with torch.no_grad():
         gi, gt = blk.forward(img.to(dev), txt.to(dev), [m.to(dev) for m in img_mods], [m.to(dev) for m in txt_mods],
                              (rope[0].to(dev), rope[1].to(dev)))
-        ri, rt = block.reference_double_stream(img_blk, txt_blk, img.to(dev), txt.to(dev),
+        ri, rt = torch_forms.reference_double_stream(img_blk, txt_blk, img.to(dev), txt.to(dev),
                                                [m.to(dev) for m in img_mods], [m.to(dev) for m in txt_mods],
                                                (rope[0].to(dev), rope[1].to(dev)))
     for got, ref in ((gi, ri), (gt, rt)):
@@ -56,3 +57,59 @@ def test_double_stream_block(dev, per_token):
         assert err < 2e-2, err
         # and the block really changed the stream (a wiring mistake that drops a branch fails here)
         assert ((got.float() - (img if got is gi else txt).to(dev).float()).norm() / ref.norm()).item() > 1e-2
+
+
+def make_linear_on(dev, gen, n, k, per_channel):
+    """Random int8 codes, fp32 scales ([N, 1] per channel or [N, K/128]) and bf16 bias, drawn on `dev`."""
+    from hy_nomas import block
+
+    qw = torch.randint(-127, 128, (n, k), generator=gen, device=dev, dtype=torch.int8)
+    sw = torch.rand(n, 1 if per_channel else k // 128, generator=gen, device=dev) * 2e-3 + 5e-4
+    bias = (torch.randn(n, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    return block.Int8Linear(qw, sw.float(), bias)
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+def test_double_stream_block_full_size(dev, per_token):
+    """The config-4 block at its real size: hidden 3072, 24 heads x 128, FFN 12288, 57344 image tokens on a
+    14 x 64 x 64 RoPE grid plus 256 text tokens, both activation layouts.  The float32 reference (dequantized
+    weights, unquantized activations, hy_nomas/model.py:230-303) computes q/k/v for every token and the
+    attention and row-local rest of the block for sampled rows of each stream; the int8 block's rows must
+    match within 2e-2 relative (as the small-block test), and so must the block's change to the stream."""
+    from hy_nomas import block
+    from oracle import torch_forms
+
+    d, heads, mlp, lv, lt = 3072, 24, 12288, 57344, 256
+    print(f"double-stream block full size per_token={per_token} ({lv}+{lt} tokens)", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(2024 + per_token)
+
+    def stream():
+        lins = [make_linear_on(dev, gen, n, k, per_token) for n, k in ((3 * d, d), (d, d), (mlp, d), (d, mlp))]
+        qn = (torch.rand(d // heads, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+        kn = (torch.rand(d // heads, generator=gen, device=dev) + 0.5).to(torch.bfloat16)
+        return block.DiTBlockInt8(*lins, qn, kn, heads, per_token=per_token)
+
+    img_blk, txt_blk = stream(), stream()
+    img = torch.randn(1, lv, d, generator=gen, device=dev).to(torch.bfloat16)
+    txt = torch.randn(1, lt, d, generator=gen, device=dev).to(torch.bfloat16)
+    img_mods = [(torch.randn(1, d, generator=gen, device=dev) * 0.1).to(torch.bfloat16) for _ in range(6)]
+    txt_mods = [(torch.randn(1, d, generator=gen, device=dev) * 0.1).to(torch.bfloat16) for _ in range(6)]
+    rope = torch_forms.rope_freqs([16, 56, 56], 256, 14, 64, 64, device=dev)
+    blk = block.DoubleStreamBlockInt8(img_blk, txt_blk)
+    with torch.no_grad():
+        gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope)
+        torch.cuda.synchronize()
+        g = seeded(55 + per_token)
+        img_rows = sorted(set(torch.randperm(lv, generator=g)[:30].tolist() + [0, lv - 1]))
+        txt_rows = sorted(set(torch.randperm(lt, generator=g)[:30].tolist() + [0, lt - 1]))
+        ri, rt = torch_forms.double_stream_rows(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope, img_rows,
+                                                txt_rows)
+    assert gi.shape == (1, lv, d) and gt.shape == (1, lt, d) and gi.dtype == torch.bfloat16
+    for name, got, x, rows, ref in (("img", gi, img, img_rows, ri), ("txt", gt, txt, txt_rows, rt)):
+        got_r, x_r = got[0, rows].float(), x[0, rows].float()
+        err = ((got_r - ref).norm() / ref.norm()).item()
+        delta_err = ((got_r - ref).norm() / (ref - x_r).norm()).item()
+        print(f"  {name}: relative error {err:.3e}, of the block's change {delta_err:.3e}", flush=True)
+        assert torch.isfinite(got_r).all()
+        assert err < 2e-2, err
+        assert delta_err < 2e-2, delta_err

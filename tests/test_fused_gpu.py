@@ -34,13 +34,14 @@ def test_adaln(dev, b, l, d, norm):
 
 def test_adaln_matches_torch(dev):
     """hy_nomas tests/test_fused.py:12-21 against torch's F.layer_norm + modulate on the CPU."""
-    from hy_nomas import block, fused
+    from hy_nomas import fused
+    from oracle import torch_forms
 
     g = seeded(1)
     x = bf(torch.randn(2, 2048, 777, generator=g) * 3).transpose(1, 2)
     shift = bf(torch.randn(2, 2048, generator=g))
     scale = bf(torch.randn(2, 2048, generator=g))
-    ref = bf(block.modulate(block.layer_norm(x), shift, scale))
+    ref = bf(torch_forms.modulate(torch_forms.layer_norm(x), shift, scale))
     got = fused.adaln(x.to(dev), shift.to(dev), scale.to(dev)).cpu()
     assert (got != ref).float().mean().item() < 1e-3
     assert (got.float() - ref.float()).abs().max().item() < 0.05
@@ -93,18 +94,19 @@ def test_gated_residual_bit_exact(dev, b, l, d):
 
 def test_qk_norm_rope(dev):
     """hy_nomas tests/test_fused.py:24-40 tolerances, against torch RMSNorm + apply_rope and the oracle."""
-    from hy_nomas import block, fused
+    from hy_nomas import fused
+    from oracle import torch_forms
 
     b, l, h, d = 2, 96, 16, 128
     g = seeded(3)
     lin = bf(torch.randn(b, l, h * d, generator=g) * 5)
     x = lin.view(b, l, h, d)
-    norm = block.RMSNorm(d).bfloat16()
+    norm = torch_forms.RMSNorm(d).bfloat16()
     with torch.no_grad():
         norm.weight.copy_(torch.rand(d, generator=g) + 0.5)
-    rope = block.rope_freqs([16, 56, 56], 256, 4, 4, 6)
+    rope = torch_forms.rope_freqs([16, 56, 56], 256, 4, 4, 6)
     with torch.no_grad():
-        ref = block.apply_rope(norm(x).to(torch.bfloat16), *rope)
+        ref = torch_forms.apply_rope(norm(x).to(torch.bfloat16), *rope)
         ref_plain = norm(x).to(torch.bfloat16)
     got = fused.qk_norm_rope(x.to(dev), norm.weight.detach().to(dev), (rope[0].to(dev), rope[1].to(dev))).cpu()
     got_plain = fused.qk_norm_rope(x.to(dev), norm.weight.detach().to(dev), None).cpu()

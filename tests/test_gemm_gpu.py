@@ -358,3 +358,32 @@ def test_wrappers_reject_mismatched_operands(dev):
         with pytest.raises(RuntimeError):
             fn()
         print(f"  rejected case {i}", flush=True)
+
+
+def test_config0_half_even_chain(dev):
+    """The single W8A8 linear of the CPU-baseline workload, chained on the GPU: x bf16 [1024, 3072] ~N(0, 1)
+    with 1 % of the channels x20, per-token int8 quantization with round-half-even, per-channel int8
+    weights [3072, 3072] with fp32 scales ~U(1e-3, 5e-3), bf16 bias, bf16 out.  Codes, scales and the bf16
+    outputs equal the oracle's chain bit for bit; the outputs are within 1e-2 of the fp64 product of the
+    dequantized operands."""
+    from hy_nomas import kernels
+
+    print("config 0 chain: half-even per-token quantization -> int8 GEMM, 1024 x 3072 -> 3072", flush=True)
+    m, k, n = 1024, 3072, 3072
+    g = seeded(0)
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: k // 100]] *= 20
+    x = x.to(torch.bfloat16)
+    w, sw, bias = int8_weights(n, k, seed=1, per_channel=True)
+    qa, sa = kernels.quantize_activations(x.to(dev), "int8", None, rounding="half_even")
+    out = kernels.block_gemm(qa, sa, w.to(dev), sw.to(dev), bias.to(dev))
+    q_ref, s_ref = oracle.quantize(x, k, "int8", rounding="half_even")
+    assert np.array_equal(qa.cpu().numpy(), q_ref) and np.array_equal(sa.cpu().numpy(), s_ref)
+    # the half-even codes differ from half-away ones somewhere (ties occur at this size), so the
+    # rounding mode really reached the kernel
+    q_away, _ = oracle.quantize(x, k, "int8")
+    assert (q_away != q_ref).any()
+    ref = oracle.block_gemm(q_ref, s_ref, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    assert torch.equal(out.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+    exact = fp64_dequant_product(q_ref, s_ref, w.numpy(), sw.numpy(), bias)
+    assert max_abs_rel(out.cpu().float().numpy(), exact) < 1e-2

@@ -97,7 +97,8 @@ def test_block_from_checkpoint_runs_on_the_int8_path(dev, tmp_path):
     dequantized weights; the QKV GEMM's weight is the concatenation of the file's q, k, v."""
     from safetensors.torch import save_file
 
-    from hy_nomas import block, loader
+    from hy_nomas import loader
+    from oracle import torch_forms
 
     print("block from checkpoint", flush=True)
     g = seeded(5)
@@ -114,10 +115,10 @@ def test_block_from_checkpoint_runs_on_the_int8_path(dev, tmp_path):
     txt = torch.randn(1, lt, D, generator=g).to(torch.bfloat16).to(dev)
     img_mods = [(torch.randn(1, D, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
     txt_mods = [(torch.randn(1, D, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
-    rope = [t.to(dev) for t in block.rope_freqs([32, 48, 48], 256, 2, 8, 6)]
+    rope = [t.to(dev) for t in torch_forms.rope_freqs([32, 48, 48], 256, 2, 8, 6)]
     with torch.no_grad():
         gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope)
-        ri, rt = block.reference_double_stream(blk.img, blk.txt, img, txt, img_mods, txt_mods, rope)
+        ri, rt = torch_forms.reference_double_stream(blk.img, blk.txt, img, txt, img_mods, txt_mods, rope)
     for got, ref in ((gi, ri), (gt, rt)):
         assert ((got.float() - ref).norm() / ref.norm()).item() < 2e-2
 

@@ -312,16 +312,16 @@ def test_gated_residual_matches_torch_bf16():
 
 
 def test_qk_norm_rope_against_torch_forms():
-    from hy_nomas import block
+    from oracle import torch_forms
     b, l, h, d = 1, 96, 4, 128
     g = torch.Generator().manual_seed(16)
     x = (torch.randn(b, l, h, d, generator=g) * 5).to(torch.bfloat16)
-    norm = block.RMSNorm(d).bfloat16()
+    norm = torch_forms.RMSNorm(d).bfloat16()
     with torch.no_grad():
         norm.weight.copy_(torch.rand(d, generator=g) + 0.5)
         plain = norm(x).to(torch.bfloat16)
-        rope = block.rope_freqs([16, 56, 56], 256, 4, 4, 6)
-        roped = block.apply_rope(plain, *rope)
+        rope = torch_forms.rope_freqs([16, 56, 56], 256, 4, 4, 6)
+        roped = torch_forms.apply_rope(plain, *rope)
     got_plain = torch.from_numpy(oracle.qk_norm_rope(x, norm.weight.detach(), None)).to(torch.bfloat16)
     got = torch.from_numpy(oracle.qk_norm_rope(x, norm.weight.detach(), rope)).to(torch.bfloat16)
     assert (got_plain != plain).float().mean().item() < 1e-3
