@@ -321,6 +321,15 @@ __device__ __forceinline__ uint32_t pack2_out(float a, float b) {
 namespace hn {
 void set_error(const char* fmt, ...);
 int hip_status(hipError_t e, const char* what);
+
+// The one-call linear (linear.hip): workspace size, argument checks, and quantize-then-GEMM into a
+// workspace that holds the activation codes and scales.
+int64_t linear_workspace_bytes(int64_t M, int64_t K, int64_t group);
+int check_linear(const char* who, const void* x, int64_t M, int64_t N, int64_t K, int64_t group, int kind,
+                 const void* qw, const float* sw, const void* out);
+int run_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t group, int kind, int rounding,
+               const void* qw, int64_t ldw, const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias,
+               int bias_dtype, int64_t N, void* out, int out_dtype, int64_t ldo, uint8_t* ws, void* stream);
 }  // namespace hn
 
 #define HN_REQUIRE(cond, ...)            \

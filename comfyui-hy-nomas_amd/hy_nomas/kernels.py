@@ -85,30 +85,42 @@ def quantize_activations(x, kind="int8", group=GROUP, rounding="half_away"):
 _CODE_DTYPES = {"int8": (torch.int8,), "fp8": (torch.float8_e4m3fn, torch.uint8)}
 
 
-def _check_gemm(qa, sa, qw, sw, bias, kind):
-    """Shapes and dtypes the kernels rely on (the C ABI sees only pointers and strides): codes of the kind,
-    matching K, one activation-scale row per token, weight-scale rows for every output channel (one per
-    channel or one per 128), a bias of N values.  Raises RuntimeError."""
+def _check_weights(qw, sw, bias, kind, k, who="block_gemm"):
+    """The weight side of a GEMM: codes of the kind with K columns, weight-scale rows for every output channel
+    (one per channel or one per 128), a bias of N values.  Raises RuntimeError."""
     if kind not in _CODE_DTYPES:
         raise RuntimeError(f"kind must be 'int8' or 'fp8', got {kind!r}")
-    if qa.dim() != 2 or qw.dim() != 2 or sa.dim() != 2 or sw.dim() != 2:
-        raise RuntimeError("block_gemm: codes and scales must be 2-D")
-    if qa.dtype not in _CODE_DTYPES[kind] or qw.dtype not in _CODE_DTYPES[kind]:
-        raise RuntimeError(f"block_gemm: {kind} codes expected, got {qa.dtype} / {qw.dtype}")
-    m, k = qa.shape
+    if qw.dim() != 2 or sw.dim() != 2:
+        raise RuntimeError(f"{who}: weight codes and scales must be 2-D")
+    if qw.dtype not in _CODE_DTYPES[kind]:
+        raise RuntimeError(f"{who}: {kind} weight codes expected, got {qw.dtype}")
     n = qw.shape[0]
     if qw.shape[1] != k:
-        raise RuntimeError(f"block_gemm: activations have K={k}, weights K={qw.shape[1]}")
+        raise RuntimeError(f"{who}: activations have K={k}, weights K={qw.shape[1]}")
+    if sw.shape[0] not in (n, (n + GROUP - 1) // GROUP):
+        raise RuntimeError(f"{who}: {sw.shape[0]} weight-scale rows for {n} output channels")
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != n):
+        raise RuntimeError(f"{who}: bias of shape {tuple(bias.shape)} for {n} output channels")
+
+
+def _check_gemm(qa, sa, qw, sw, bias, kind):
+    """Shapes and dtypes the kernels rely on (the C ABI sees only pointers and strides): codes of the kind,
+    matching K, one activation-scale row per token, and the weight side (`_check_weights`)."""
+    if kind not in _CODE_DTYPES:
+        raise RuntimeError(f"kind must be 'int8' or 'fp8', got {kind!r}")
+    if qa.dim() != 2 or sa.dim() != 2:
+        raise RuntimeError("block_gemm: codes and scales must be 2-D")
+    if qa.dtype not in _CODE_DTYPES[kind]:
+        raise RuntimeError(f"block_gemm: {kind} codes expected, got {qa.dtype}")
+    m, k = qa.shape
     if sa.shape[0] != m:
         raise RuntimeError(f"block_gemm: {sa.shape[0]} activation-scale rows for {m} tokens")
-    if sw.shape[0] not in (n, (n + GROUP - 1) // GROUP):
-        raise RuntimeError(f"block_gemm: {sw.shape[0]} weight-scale rows for {n} output channels")
-    if bias is not None and (bias.dim() != 1 or bias.shape[0] != n):
-        raise RuntimeError(f"block_gemm: bias of shape {tuple(bias.shape)} for {n} output channels")
+    _check_weights(qw, sw, bias, kind, k)
 
 
-def _layout(sa, sw, n, k, kind, swiglu=False):
-    """How the GEMM reads the scales: (sw, sw_rows, group, groups).
+def _layout(sw, n, k, kind, sa_cols, sa=None, swiglu=False):
+    """How the GEMM reads the scales: (sw, sw_rows, group, groups).  `sa_cols`: activation-scale columns
+    (1 or K / 128); `sa`: the activation scales when they are not this call's own quantizer output.
 
     sw_rows = 128: one weight-scale row per 128 output channels (the fp8 block layout), read as stored by
     the per-group fold.  With fp8 codes that fold keeps its running sum in units of the current group's
@@ -119,12 +131,13 @@ def _layout(sa, sw, n, k, kind, swiglu=False):
     sw_rows = 1 if sw.shape[0] == n else GROUP
     if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
         raise RuntimeError(f"weight scales with {sw.shape[0]} rows for {n} output channels")
-    if sw_rows == GROUP and kind == "fp8" and not (_scales_positive_finite(sa) and _scales_positive_finite(sw)):
+    if sw_rows == GROUP and kind == "fp8" and not ((sa is None or _scales_positive_finite(sa))
+                                                   and _scales_positive_finite(sw)):
         if swiglu:
             raise RuntimeError("swiglu_quant: fp8 block scales must be positive and finite")
         sw = sw.float().repeat_interleave(GROUP, dim=0)[:n]
         sw_rows = 1
-    if sw_rows == 1 and sa.shape[1] == 1 and sw.shape[1] == 1 and (kind == "fp8" or k < WHOLE_K_INT32_LIMIT):
+    if sw_rows == 1 and sa_cols == 1 and sw.shape[1] == 1 and (kind == "fp8" or k < WHOLE_K_INT32_LIMIT):
         return sw, sw_rows, k, 1
     return sw, sw_rows, GROUP, k // GROUP
 
@@ -170,7 +183,7 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
         qs = None
     if m == 0:
         return (out, qs) if quantized else out
-    sw, sw_rows, group, groups = _layout(sa, sw, n, k, kind, swiglu=mode == 4)
+    sw, sw_rows, group, groups = _layout(sw, n, k, kind, sa.shape[1], sa, swiglu=mode == 4)
     sa = _scales(sa, m, groups)
     sw = _scales(sw, sw.shape[0], groups)
     qa = _rows(qa)
@@ -214,7 +227,7 @@ def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="
         raise RuntimeError(f"qkv_heads: out must be contiguous bf16 [3, {batch}, {hidden // 128}, >= {l_offset + length}, 128]")
     if m == 0:
         return out
-    sw, sw_rows, group, groups = _layout(sa, sw, n, k, kind)
+    sw, sw_rows, group, groups = _layout(sw, n, k, kind, sa.shape[1], sa)
     sa = _scales(sa, m, groups)
     sw = _scales(sw, sw.shape[0], groups)
     qa, qw = _rows(qa), _rows(qw)
@@ -282,21 +295,46 @@ def block_linear(x, qw, sw, bias=None, kind="int8"):
     """F.linear with block-scaled 8-bit weights: x [..., K] -> [..., N] in x's dtype
     (hy_nomas/kernels.py:210-222).  Weight scales [N, K/128] select per-token-and-group activation
     quantization; per-channel scales [N, 1] select per-token quantization; block scales
-    [ceil(N/128), K/128] (one row per 128 output channels) are taken as they are."""
+    [ceil(N/128), K/128] (one row per 128 output channels) are taken as they are.  One library call
+    (hn_block_linear) quantizes into a workspace and runs the GEMM."""
     shape = x.shape
     x2 = x.reshape(-1, shape[-1])
     if not x2.is_contiguous():
         x2 = x2.contiguous()
-    if shape[-1] % GROUP or x2.shape[0] == 0:
+    m, k = x2.shape
+    if k % GROUP or m == 0:
         from .ops import dequantize_g128
         if sw.shape[0] != qw.shape[0]:
             sw = sw.repeat_interleave(GROUP, dim=0)[: qw.shape[0]]
         return torch.nn.functional.linear(x, dequantize_g128(qw, sw, x.dtype), bias)
-    group = None if sw.shape[1] == 1 else GROUP
+    _lib.require_device(x, qw, sw, bias)
+    _check_weights(qw, sw, bias, kind, k, "block_linear")
+    n = qw.shape[0]
+    group = k if sw.shape[1] == 1 else GROUP
+    # the activation quantizer's scales are positive (finite for finite x): only the weight scales are checked
+    sw, sw_rows, gemm_group, groups = _layout(sw, n, k, kind, k // group)
+    if gemm_group != group:
+        # per-token scales over a K the int32 sum cannot hold: quantize per token, fold per group
+        with torch.cuda.device(x.device):
+            qa, sa = quantize_activations(x2, kind, None)
+            out = block_gemm(qa, sa, qw, sw, bias, x.dtype, kind)
+        return out.reshape(*shape[:-1], n)
+    if x2.dtype not in _lib.DTYPE:
+        x2 = x2.float()
+    x2 = _rows(x2)
+    sw = _scales(sw, sw.shape[0], groups)
+    qw = _rows(qw)
+    if bias is not None and not bias.is_contiguous():
+        bias = bias.contiguous()
+    out = torch.empty((m, n), device=x.device, dtype=x.dtype if x.dtype in _lib.DTYPE else torch.float32)
+    nbytes = _lib.lib().hn_block_linear_workspace_bytes(m, k, group)
+    ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
     with torch.cuda.device(x.device):
-        qa, sa = quantize_activations(x2, kind, group)
-        out = block_gemm(qa, sa, qw, sw.float(), bias, x.dtype, kind)
-    return out.reshape(*shape[:-1], qw.shape[0])
+        _lib.call("hn_block_linear", x2.data_ptr(), _lib.dtype_code(x2), x2.stride(0), m, k, group, _lib.KIND[kind],
+                  _lib.ROUND["half_away"], qw.data_ptr(), qw.stride(0), sw.data_ptr(), sw.stride(0), sw_rows,
+                  _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0, n, out.data_ptr(),
+                  _lib.dtype_code(out), out.stride(0), ws.data_ptr(), nbytes, _lib.stream(x2))
+    return out.reshape(*shape[:-1], n).to(x.dtype)
 
 
 def int8_g128_linear(x, qw, sw, bias=None):

@@ -72,7 +72,8 @@ int hn_quantize_act(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * of the FP8 block-128 weight layout (hy_nomas/pixelumm.py:60-63, 77-82) without the repeat_interleave
  * its fp8 linear applies before block_linear (pixelumm.py:147-152); the fold is then
  * acc = fma(part, sa * sw, acc).
- * group = 128 (the reference's g128 layout) or K (per-token activations x per-channel weights).
+ * group = 128 (the reference's g128 layout) or K (per-token activations x per-channel weights); with int8
+ * codes, group = K (and ACC32) needs K < 131072, so that the whole-K int32 sum cannot overflow.
  * epilogue NONE: out [M, N] of out_dtype.  GELU: out = bf16(gelu_tanh(bf16(acc))) (kernels.py:125-128).
  * GELU_QUANT: out int8 [M, N] codes of the GELU output, quantized per row and 128 columns, with scales
  * qs [M, N / 128] (kernels.py:129-137); N % 128 == 0.  ACC32: out int32 [M, N] = full-K integer dot
@@ -91,6 +92,25 @@ int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64_t ldsa, co
                   const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K,
                   int64_t group, int kind, int epilogue, void* out, int out_dtype, int64_t ldo, float* qs,
                   int64_t ldqs, void* stream);
+
+/*
+ * W8A8 linear in one call: dynamic activation quantization (as hn_quantize_act) followed by the block-scaled
+ * GEMM (as hn_block_gemm, epilogue NONE).  Replaces kernels.block_linear (hy_nomas/kernels.py:210-222) for
+ * K % 128 == 0 and M > 0; the reference's dequantize + F.linear fallback for other shapes stays with the
+ * caller.
+ *   x [M, K] (x_dtype, row stride ldx) is quantized per token and `group` channels (128: the reference;
+ *   K: one scale per token) with `kind` codes and `rounding`; the codes and scales are written to
+ *   `workspace` (256-byte aligned, at least hn_block_linear_workspace_bytes(M, K, group) bytes; its contents
+ *   on entry do not matter and are overwritten) and multiplied with qw / sw / bias as hn_block_gemm does,
+ *   into out [M, N] of out_dtype (row stride ldo).
+ * With kind FP8 and sw_rows == 128 the weight scales must be positive and finite.
+ */
+int64_t hn_block_linear_workspace_bytes(int64_t M, int64_t K, int64_t group);
+
+int hn_block_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t group, int kind,
+                    int rounding, const void* qw, int64_t ldw, const float* sw, int64_t ldsw, int64_t sw_rows,
+                    const void* bias, int bias_dtype, int64_t N, void* out, int out_dtype, int64_t ldo,
+                    void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * The QKV projection of a double-stream block with QK-norm and RoPE in its epilogue, written head-major

@@ -199,7 +199,7 @@ def test_whole_k_int8_routes_long_k_to_the_group_fold(monkeypatch):
     hands it to the per-group fold instead (scales repeated per group); shorter K keeps whole-K mode."""
     from hy_nomas import kernels
 
-    sa, sw = torch.ones(4, 1), torch.ones(8, 1)
-    assert kernels._layout(sa, sw, 8, 3072, "int8")[2:] == (3072, 1)
-    assert kernels._layout(sa, sw, 8, 131072, "int8")[2:] == (128, 1024)
-    assert kernels._layout(sa, sw, 8, 131072, "fp8")[2:] == (131072, 1)
+    sw = torch.ones(8, 1)
+    assert kernels._layout(sw, 8, 3072, "int8", 1)[2:] == (3072, 1)
+    assert kernels._layout(sw, 8, 131072, "int8", 1)[2:] == (128, 1024)
+    assert kernels._layout(sw, 8, 131072, "fp8", 1)[2:] == (131072, 1)
