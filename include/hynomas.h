@@ -113,6 +113,23 @@ int hn_block_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * hn_block_linear without a workspace argument and without allocating: the activation codes and scales go
+ * to a scratch array of HN_NOALLOC_SCRATCH_BYTES in device memory that the library holds on each GPU it
+ * runs on until the process ends.  No counterpart in the reference: this entry point is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * Arguments and results are those of hn_block_linear; a problem needing more than
+ * HN_NOALLOC_SCRATCH_BYTES (hn_block_linear_workspace_bytes(M, K, group)) is rejected with HN_ERR_ARG.
+ * All calls on one GPU share its array: calls that overlap on one GPU (other streams or threads) race,
+ * and must be serialized by the caller.
+ */
+#define HN_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+int hn_block_linear_noalloc(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int64_t group, int kind,
+                            int rounding, const void* qw, int64_t ldw, const float* sw, int64_t ldsw, int64_t sw_rows,
+                            const void* bias, int bias_dtype, int64_t N, void* out, int out_dtype, int64_t ldo,
+                            void* stream);
+
+/*
  * The QKV projection of a double-stream block with QK-norm and RoPE in its epilogue, written head-major
  * for attention.  Replaces the block_gemm of the three q/k/v linears plus the two fused.qk_norm_rope
  * calls of DoubleStreamBlock._qkv (hy_nomas/model.py:253-267, fused.py:65-105), and the [B, L, H, D] ->
