@@ -452,7 +452,10 @@ void block_gemm_kernel(const GemmArgs a) {
     // products of weight fragments [i0, i1) with every activation fragment of register set `set`
     // rs (RESCALE, a stage's first slice): each accumulator block is moved to this group's scale product
     // just before its first product of the stage, 16 multiplies per block interleaved with the matrix core
-    auto mfma_rows = [&](int set, int i0, int i1, const float* rs = nullptr) __attribute__((always_inline)) {
+    // fresh: the group's first products, which start the partial from zero (the inline constant 0 as the
+    // accumulator operand) instead of adding to a zeroed set
+    auto mfma_rows = [&](int set, int i0, int i1, const float* rs = nullptr, bool fresh = false)
+        __attribute__((always_inline)) {
 #pragma unroll
       for (int i = i0; i < i1; i++)
 #pragma unroll
@@ -461,7 +464,8 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] *= rs[j];
           }
-          acc[i][j] = MF::run(fa[set][i], fb[set][j], acc[i][j]);
+          if (fresh) acc[i][j] = MF::run(fa[set][i], fb[set][j], Acc{});
+          else acc[i][j] = MF::run(fa[set][i], fb[set][j], acc[i][j]);
         }
       if (rs) {
 #pragma unroll
@@ -484,6 +488,9 @@ void block_gemm_kernel(const GemmArgs a) {
     // after it (1.7 % faster over the DiT stack); the g128 and block-scale tiles keep one row before it
     // (none there is 0.5 % and 3 % slower, two 0.4 % and 2.5 % slower).
     constexpr int PRE = G128 ? 1 : 0;
+    // the g128 fold (not the rescaled running sum) with one group per stage: every stage starts its partials
+    // in its first products, so the fold leaves them as they are
+    constexpr bool FRESH = G128 && !RESCALE && STAGES_PER_GROUP == 1;
     constexpr int POST_MFMA = (TN - PRE) * TM;
     constexpr int VM_LOADS = A_KB + B_KB + SC_PER_WAVE;
     constexpr int VM_PER = (VM_LOADS + POST_MFMA - 1) / POST_MFMA;  // POST_MFMA >= TM > 0
@@ -509,17 +516,19 @@ void block_gemm_kernel(const GemmArgs a) {
       for (int s = 0; s < SLICES; s++) {
         const int cur = s & 1;
         const float* rsc = RESCALE && s == 0 ? rs : nullptr;
+        // g128 fold with one group per stage: the stage's first slice starts every partial afresh
+        const bool fresh = FRESH && s == 0;
         if (s + 1 < SLICES) {
-          mfma_rows(cur, 0, 1, rsc);
+          mfma_rows(cur, 0, 1, rsc, fresh);
           __builtin_amdgcn_sched_barrier(0x6);
           read_frags(cur ^ 1, stage, s + 1);
           __builtin_amdgcn_sched_barrier(0x6);
-          mfma_rows(cur, 1, TN, rsc);
+          mfma_rows(cur, 1, TN, rsc, fresh);
           __builtin_amdgcn_sched_barrier(0x6);
         } else if constexpr (MODE == 2) {
-          mfma_rows(cur, 0, TN);
+          mfma_rows(cur, 0, TN, nullptr, fresh);
         } else {
-          mfma_rows(cur, 0, PRE);
+          mfma_rows(cur, 0, PRE, nullptr, fresh);
           // (the waits and the barrier are scalar instructions: nothing may cross them)
           __builtin_amdgcn_sched_barrier(0);
           // stage kt + 1 (the only loads in flight) has landed for this wave and its reads of stage kt
@@ -530,7 +539,7 @@ void block_gemm_kernel(const GemmArgs a) {
           __builtin_amdgcn_sched_barrier(0);
           read_frags(cur ^ 1, smem + SCR + (buf ^ 1) * STAGE, 0);
           if constexpr (MODE == 0) issue_stage(kt + 2, buf);
-          mfma_rows(cur, PRE, TN);
+          mfma_rows(cur, PRE, TN, nullptr, fresh);
           // reads first, then products and loads alternating
           __builtin_amdgcn_sched_group_barrier(0x100, TN + TM, 0);
 #pragma unroll
@@ -578,12 +587,14 @@ void block_gemm_kernel(const GemmArgs a) {
               }
             }
           }
+          if constexpr (!FRESH) {
 #pragma unroll
-          for (int i = 0; i < TN; i++)
+            for (int i = 0; i < TN; i++)
 #pragma unroll
-            for (int j = 0; j < TM; j++)
+              for (int j = 0; j < TM; j++)
 #pragma unroll
-              for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+          }
         }
       }
     };
