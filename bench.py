@@ -321,9 +321,10 @@ def rope_tables(length, head_dim, gen, dev):
 def dit_block(dev, gen, steps, warmup, per_token):
     """One synthetic double-stream DiT block forward (hy_nomas/model.py:230-286) at hidden 3072, 24 heads x 128,
     FFN 12288 GELU-tanh: 57344 image tokens (RoPE grid 14 x 64 x 64) + 256 text tokens, random int8 weights,
-    joint torch SDPA attention.  Returns {"block_ms", "attention_ms", "linear_path_ms", "linear_TOPS"}; the linear
-    path (every kernel of this package) is the block time minus the attention time of the same shapes."""
-    from hy_nomas import block
+    joint attention with torch SDPA (the default) and with the HIP attention kernel.  For each backend:
+    {"block_ms", "attention_ms", "linear_path_ms", "linear_TOPS"}; the linear path (every other kernel of this
+    package) is the block time minus the attention time of the same shapes, timed as the block calls it."""
+    from hy_nomas import attention, block
 
     d, heads, mlp, lv, lt = HIDDEN, 24, 12288, 57344, 256
 
@@ -345,19 +346,25 @@ def dit_block(dev, gen, steps, warmup, per_token):
     mods = [[(torch.randn(1, d, generator=gen, device=dev) * 0.1).to(torch.bfloat16) for _ in range(6)]
             for _ in range(2)]
     rope = rope_tables(lv, d // heads, gen, dev)
-    with torch.no_grad():
-        ms, _ = time_launches([lambda: blk.forward(img, txt, mods[0], mods[1], rope)], steps, warmup)
-        # the block's attention call on the same operands: head-major q, k, v [B, H, L, D] as the QKV
-        # epilogue writes them (no layout copies), image and text tokens together
-        hm = torch.randn(3, 1, heads, lv + lt, d // heads, generator=gen, device=dev).to(torch.bfloat16)
-        att_ms, _ = time_launches([lambda: block.attention_heads(hm[0], hm[1], hm[2])], steps, warmup)
+    out = {"activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
     ops = 2 * (lv + lt) * sum(n * k for _, k, n in STACK)
-    lin_ms = ms - att_ms
+    # the block's attention call on the same operands: head-major q, k, v [B, H, L, D] as the QKV epilogue
+    # writes them, image and text tokens together
+    hm = torch.randn(3, 1, heads, lv + lt, d // heads, generator=gen, device=dev).to(torch.bfloat16)
+    att_flops = 4 * (lv + lt) ** 2 * d
+    with torch.no_grad():
+        for backend in ("sdpa", "hip"):
+            ms, _ = time_launches([lambda: blk.forward(img, txt, mods[0], mods[1], rope, backend)], steps, warmup)
+            att_ms, _ = time_launches([lambda: attention.attention_heads(hm[0], hm[1], hm[2], backend)], steps, warmup)
+            lin_ms = ms - att_ms
+            out[backend] = {"block_ms": round(ms, 3), "attention_ms": round(att_ms, 3),
+                            "attention_TFLOPS": round(att_flops / (att_ms * 1e-3) / 1e12, 1),
+                            "linear_path_ms": round(lin_ms, 3), "linear_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1)}
     del blk, img, txt, hm
     torch.cuda.empty_cache()
-    return {"block_ms": round(ms, 3), "attention_ms": round(att_ms, 3), "linear_path_ms": round(lin_ms, 3),
-            "linear_ops": ops, "linear_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1),
-            "activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
+    out["linear_ops"] = ops
+    out["attention_flops"] = att_flops
+    return out
 
 
 # the linears of the reference's own kernel benchmark (dev/bench_kernels.py:27-28): the released checkpoint's

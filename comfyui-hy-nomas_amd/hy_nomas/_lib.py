@@ -37,6 +37,8 @@ SIGNATURES = {
                          _p, _i64, _p], _i),
     "hn_block_linear_noalloc": ([_p, _i, _i64, _i64, _i64, _i64, _i, _i, _p, _i64, _p, _i64, _i64, _p, _i, _i64, _p,
                                  _i, _i64, _p], _i),
+    "hn_attention": ([_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64,
+                      _i64, _i64, _i64, _i64, _f, _p], _i),
     "hn_adaln": ([_p, _p, _p, _i, _i64, _i64, _i64, _f, _i, _p, _p], _i),
     "hn_adaln_quant": ([_p, _p, _p, _i, _i64, _i64, _i64, _f, _i, _i, _i64, _p, _p, _p], _i),
     "hn_gated_residual": ([_p, _p, _p, _i, _i64, _i64, _i64, _p, _p], _i),

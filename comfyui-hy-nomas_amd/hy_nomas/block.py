@@ -9,6 +9,7 @@ requantization epilogue -> int8 FFN-down -> gated residual.
 import torch
 import torch.nn.functional as F
 
+from . import attention as attn
 from . import fused, kernels
 
 
@@ -63,22 +64,13 @@ class DiTBlockInt8:
         h = kernels.block_gemm(qh, sh, self.fc2.qw, self.fc2.sw, self.fc2.bias, out_dtype=x.dtype)
         return fused.gated_residual(x, h.view_as(x), gate2)
 
-    def forward(self, x, mods, rope=None):
-        """Self-attention over this stream only (torch SDPA, unchanged), then `post`."""
+    def forward(self, x, mods, rope=None, backend=None):
+        """Self-attention over this stream only (`attention.attention_heads`: torch SDPA by default, or the HIP
+        kernel), then `post`."""
         shift1, scale1, gate1, shift2, scale2, gate2 = mods
         hm = self.attention_heads(x, shift1, scale1, rope)
-        attn = attention_heads(hm[0], hm[1], hm[2]).reshape(x.shape)
-        return self.post(x, attn, gate1, shift2, scale2, gate2)
-
-
-def attention_heads(qh, kh, vh):
-    """`attention` on head-major operands qh, kh, vh [B, H, L, D] (contiguous, as the QKV epilogue writes
-    them): no layout copies before SDPA.  Returns [B, L, H, D] (a view of SDPA's output)."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-
-    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-        out = F.scaled_dot_product_attention(qh, kh, vh)
-    return out.transpose(1, 2)
+        out = attn.attention_heads(hm[0], hm[1], hm[2], backend).reshape(x.shape)
+        return self.post(x, out, gate1, shift2, scale2, gate2)
 
 
 class DoubleStreamBlockInt8:
@@ -91,7 +83,8 @@ class DoubleStreamBlockInt8:
     def __init__(self, img, txt):
         self.img, self.txt = img, txt
 
-    def forward(self, img, txt, img_mods, txt_mods, rope=None):
+    def forward(self, img, txt, img_mods, txt_mods, rope=None, backend=None):
+        """`backend`: the attention backend ("sdpa", "hip"; None: HY_NOMAS_ATTENTION, else "sdpa")."""
         shift1, scale1, gate1, shift2, scale2, gate2 = img_mods
         tshift1, tscale1, tgate1, tshift2, tscale2, tgate2 = txt_mods
         b, lv = img.shape[0], img.shape[1]
@@ -101,9 +94,9 @@ class DoubleStreamBlockInt8:
                          device=img.device, dtype=torch.bfloat16)
         self.img.attention_heads(img, shift1, scale1, rope, out=hm, l_offset=0)
         self.txt.attention_heads(txt, tshift1, tscale1, None, out=hm, l_offset=lv)
-        attn = attention_heads(hm[0], hm[1], hm[2])
+        out = attn.attention_heads(hm[0], hm[1], hm[2], backend)
         del hm
-        attn = attn.reshape(b, attn.shape[1], -1)
-        img = self.img.post(img, attn[:, :lv], gate1, shift2, scale2, gate2)
-        txt = self.txt.post(txt, attn[:, lv:], tgate1, tshift2, tscale2, tgate2)
+        out = out.reshape(b, out.shape[1], -1)
+        img = self.img.post(img, out[:, :lv], gate1, shift2, scale2, gate2)
+        txt = self.txt.post(txt, out[:, lv:], tgate1, tshift2, tscale2, tgate2)
         return img, txt

@@ -150,6 +150,22 @@ int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, con
                  int64_t L_total, int64_t l_offset, void* stream);
 
 /*
+ * Softmax attention over all keys (no mask).  Replaces the scaled-dot-product attention of the double-stream
+ * block (hy_nomas/model.py:145-150 `attention`, which hands q / k / v [B, L, H, D] to ComfyUI's backend),
+ * and each query group's call in segment_attention (model.py:199-223) once the caller has gathered that
+ * group's keys.
+ *   out[b, i, h, :] = sum_j softmax_j(scale * q[b, i, h, :] . k[b, j, h, :]) v[b, j, h, :]
+ * bf16 q, k, out with head dim D == 128 (contiguous), any element strides of batch / head / token;
+ * V is given transposed: vt[b, h, d, j] at vt + b svb + h svh + d svd + j, and every V^T row must be readable
+ * up to ceil(Lk / 64) * 64 keys with finite values past Lk (svd >= that; zeros are the usual padding).
+ * fp32 scores and softmax, bf16 probabilities in the second product, bf16 out.  Lk >= 1.
+ */
+int hn_attention(const void* q, int64_t sqb, int64_t sqh, int64_t sqi, const void* k, int64_t skb, int64_t skh,
+                 int64_t skj, const void* vt, int64_t svb, int64_t svh, int64_t svd, void* out, int64_t sob,
+                 int64_t soh, int64_t soi, int64_t B, int64_t H, int64_t Lq, int64_t Lk, int64_t D, float scale,
+                 void* stream);
+
+/*
  * LayerNorm (or RMSNorm) + adaLN modulate.  Replaces fused.adaln / _adaln_kernel (hy_nomas/fused.py:37-62).
  *   x [B, L, D] contiguous (x_dtype bf16 or fp16), shift/scale [B, D] -> y [B, L, D] (same dtype):
  *   y = norm(x) * bf16(1 + scale[b]) + shift[b].

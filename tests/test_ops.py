@@ -203,3 +203,25 @@ def test_whole_k_int8_routes_long_k_to_the_group_fold(monkeypatch):
     assert kernels._layout(sw, 8, 3072, "int8", 1)[2:] == (3072, 1)
     assert kernels._layout(sw, 8, 131072, "int8", 1)[2:] == (128, 1024)
     assert kernels._layout(sw, 8, 131072, "fp8", 1)[2:] == (131072, 1)
+
+
+def test_attention_backend_selection_and_value_layout(monkeypatch):
+    """The attention backend switch (HY_NOMAS_ATTENTION) and the kernel's V^T layout: keys contiguous, padded
+    with zeros up to the 64-key tile."""
+    from hy_nomas import attention
+
+    monkeypatch.delenv(attention.BACKEND_ENV, raising=False)
+    assert attention.backend() == "sdpa" and attention.backend("hip") == "hip"
+    monkeypatch.setenv(attention.BACKEND_ENV, "hip")
+    assert attention.backend() == "hip" and attention.backend("sdpa") == "sdpa"
+    monkeypatch.setenv(attention.BACKEND_ENV, "flash")
+    with pytest.raises(ValueError):
+        attention.backend()
+    vh = torch.randn(2, 3, 70, 128).to(torch.bfloat16)
+    vt = attention.transpose_values(vh)
+    assert vt.shape == (2, 3, 128, 128)
+    assert torch.equal(vt[..., :70], vh.transpose(-1, -2)) and not vt[..., 70:].any()
+    k = torch.randn(1, 5, 2, 128)
+    hk = torch.randn(1, 3, 2, 128)
+    keys, vals = attention._keys([(hk, hk + 1), None, (k, k + 1), (k[:, :0], k[:, :0])])
+    assert torch.equal(keys, torch.cat([hk, k], dim=1)) and torch.equal(vals, torch.cat([hk + 1, k + 1], dim=1))
