@@ -367,6 +367,24 @@ def dit_block(dev, gen, steps, warmup, per_token):
     return out
 
 
+def attention_only(dev, gen, steps, warmup):
+    """The block's joint attention alone at 57344 + 256 tokens x 24 heads x 128 (head-major bf16 q, k, v as the
+    QKV epilogue writes them), on both backends: ms and TFLOPS (4 L^2 D H flops)."""
+    from hy_nomas import attention
+
+    length, heads = 57344 + 256, 24
+    hm = torch.randn(3, 1, heads, length, 128, generator=gen, device=dev).to(torch.bfloat16)
+    flops = 4 * length ** 2 * 128 * heads
+    out = {"tokens": length, "heads": heads, "flops": flops}
+    with torch.no_grad():
+        for backend in ("sdpa", "hip"):
+            ms, _ = time_launches([lambda: attention.attention_heads(hm[0], hm[1], hm[2], backend)], steps, warmup)
+            out[backend] = {"ms": round(ms, 3), "TFLOPS": round(flops / (ms * 1e-3) / 1e12, 1)}
+    del hm
+    torch.cuda.empty_cache()
+    return out
+
+
 # the linears of the reference's own kernel benchmark (dev/bench_kernels.py:27-28): the released checkpoint's
 # hidden 2048 / FFN 8192 DiT at 26400 tokens, the PixelUMM decoder's 4096 <-> 12288 MLP at 35200, and an M=300
 # text-length case; weights N(0, 0.02) in Tencent's g128 int8 layout, activations N(0, 2)
@@ -671,7 +689,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--block-only", action="store_true", help="only the DiT block forward (both layouts)")
-    ap.add_argument("--only", choices=["fp8", "g128", "elementwise", "peaks", "refshapes", "config0"],
+    ap.add_argument("--only", choices=["fp8", "g128", "elementwise", "peaks", "refshapes", "config0", "attention"],
                     help="only one of the extra measurements (for per-kernel profiling runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 512 MiB five times (HBM counter calibration)")
@@ -714,6 +732,9 @@ def main():
         return
     if args.only == "config0":
         print(json.dumps({"config0_gpu": config0_gpu(dev, args.steps, args.warmup)}))
+        return
+    if args.only == "attention":
+        print(json.dumps({"attention": attention_only(dev, gen, max(3, args.steps // 4), 1)}))
         return
     if args.only == "elementwise":
         print(json.dumps(elementwise(dev, gen, max(10, args.steps), 3)))

@@ -13,16 +13,24 @@
 //
 // Layouts.  The scores are computed transposed, S^T = K Q^T (keys as the MFMA A rows, queries as the B
 // columns), so each lane's accumulators hold one query and 16 keys of each 32-key block: the row statistics
-// of a query are in-lane sums plus one exchange with lane l ^ 32, which holds the other 16 keys.  Each lane
-// keeps its own partial row sum and the two are added once at the end.  The output is accumulated transposed
-// too, O^T = V^T P^T, with the probabilities as the B operand straight from the score registers: an MFMA's
-// operands run along the reduced dimension (here the keys), so the 16 keys of a B fragment are taken in the
-// order the score accumulators hold them, and the V^T fragment reads the same keys, two runs of 4.  V is
-// therefore read from V^T (keys contiguous for each of the 128 dims).
+// of a query are in-lane reductions plus one exchange with lane l ^ 32, which holds the other 16 keys.  Each
+// lane keeps its own partial row sum and the two are added once at the end.  The output is accumulated
+// transposed too, O^T = V^T P^T, with the probabilities as the B operand straight from the score registers:
+// an MFMA's operands run along the reduced dimension (here the keys), so the 8 keys of a lane's B fragment
+// are the ones its score registers hold, keys 16 g + 8 (e / 4) + 4 h + e % 4 (e = 0..7) of 16-key group g in
+// lane half h.  V^T therefore comes with the keys of each 16-key group stored in the order 0-3, 8-11, 4-7,
+// 12-15 (`hn_attention`'s V^T layout): lane half h's 8 keys are then one 16-byte chunk, read with one
+// ds_read_b128.
 //
-// LDS.  K tile: 64 rows of 256 bytes, 16-byte chunk c of row r at c ^ (r & 15); V^T tile: 128 rows of 128 bytes,
-// chunk c of row r at c ^ ((r >> 1) & 7).  The direct loads write 1 KB per wave instruction in lane order, so
-// the swizzle is applied on the global side (the lane fetches the logical chunk of its physical slot).
+// LDS.  K tile: 64 rows of 256 bytes, 16-byte chunk c of row r at c ^ (r & 15); V^T tile: 128 rows of 128
+// bytes, chunk c of row r at c ^ ((r >> 1) & 7).  Both are read conflict-free (16 lanes per 256-byte pass hit
+// 16 different bank quads).  The direct loads write 1 KB per wave instruction in lane order, so the swizzle
+// is applied on the global side (the lane fetches the logical chunk of its physical slot).
+//
+// Lazy rescale.  The running reference max m moves only when a tile's max exceeds it by more than 8 (base-2
+// units), so the probabilities exp2(s - m) stay below 2^8 and the accumulators are rescaled only a few times
+// per query instead of whenever the max grows.  The result is the same quotient: numerator and denominator
+// share the reference.
 #include "hn_common.h"
 
 namespace hn {
@@ -30,6 +38,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int v4i_a __attribute__((ext_vector_type(4)));
+typedef float v16f_a __attribute__((ext_vector_type(16)));
 
 constexpr int kHeadDim = 128;
 constexpr int kBQ = 128;                        // queries per workgroup
@@ -38,13 +47,14 @@ constexpr int kAttnWaves = 4;
 constexpr int kKTile = kBK * kHeadDim * 2;      // 16 KB
 constexpr int kVTile = kHeadDim * kBK * 2;      // 16 KB
 constexpr int kAttnStage = kKTile + kVTile;
+constexpr float kSlack = 8.0f;                  // headroom of the lazy max (base-2 units)
 
 struct AttnArgs {
   const uint16_t* q;
   int64_t sqb, sqh, sqi;  // element strides of batch, head, token (dims contiguous)
   const uint16_t* k;
   int64_t skb, skh, skj;
-  const uint16_t* vt;     // V^T: element (b, h, d, j) at vt + b svb + h svh + d svd + j
+  const uint16_t* vt;     // V^T: element (b, h, d, key position p) at vt + b svb + h svh + d svd + p
   int64_t svb, svh, svd;
   uint16_t* o;
   int64_t sob, soh, soi;
@@ -62,18 +72,25 @@ __device__ __forceinline__ void g2lds16_a(const void* g, char* lds_wave_base) {
 
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
-__device__ __forceinline__ float fmax_f(float a, float b) { return __builtin_fmaxf(a, b); }
+// max of x over lanes l and l ^ 32 (one v_permlane32_swap instead of an LDS permute)
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  return __builtin_fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
 
 __global__ __launch_bounds__(kAttnWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attention_kernel(const AttnArgs a) {
   __shared__ __align__(16) char smem[2 * kAttnStage];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h2 = lane >> 5, l32 = lane & 31;
   const int bh = blockIdx.x / a.qblocks, qb = blockIdx.x % a.qblocks;
   const int64_t b = bh / a.H, hh = bh % a.H;
   const uint16_t* qbase = a.q + b * a.sqb + hh * a.sqh;
-  const uint16_t* kbase = a.k + b * a.skb + hh * a.skh;
-  const uint16_t* vbase = a.vt + b * a.svb + hh * a.svh;
+  const char* kbase = reinterpret_cast<const char*>(a.k + b * a.skb + hh * a.skh);
+  const char* vbase = reinterpret_cast<const char*>(a.vt + b * a.svb + hh * a.svh);
+  const uint32_t kstride = (uint32_t)(a.skj * 2), vstride = (uint32_t)(a.svd * 2);  // bytes per key / dim row
   const int64_t q0 = (int64_t)qb * kBQ + wave * 32;
   const int64_t qi = q0 + l32 < a.Lq ? q0 + l32 : a.Lq - 1;
 
@@ -83,35 +100,46 @@ void attention_kernel(const AttnArgs a) {
   for (int ks = 0; ks < 8; ks++) qf[ks] = *reinterpret_cast<const bf16x8*>(qbase + qi * a.sqi + 16 * ks + 8 * h2);
 
   // direct loads of one tile: wave w fills the 1 KB blocks w, w + 4, w + 8, w + 12 of the K tile (4 rows of
-  // 256 bytes each) and of the V^T tile (8 rows of 128 bytes)
+  // 256 bytes each) and of the V^T tile (8 rows of 128 bytes), each lane 16 bytes at a 32-bit offset from a
+  // wave-uniform base
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int krow = (wave + 4 * u) * 4 + lane / 16, kphys = lane % 16;
+    koff[u] = (uint32_t)krow * kstride + (uint32_t)((kphys ^ (krow & 15)) << 4);
+    const int vrow = (wave + 4 * u) * 8 + lane / 8, vphys = lane % 8;
+    voff[u] = (uint32_t)vrow * vstride + (uint32_t)((vphys ^ ((vrow >> 1) & 7)) << 4);
+  }
   auto issue_tile = [&](int64_t j0, int buf) {
     char* kt = smem + buf * kAttnStage;
     char* vt = kt + kKTile;
+    const char* kb = kbase + j0 * kstride;
+    const char* vb = vbase + j0 * 2;
+    if (j0 + kBK <= a.Lk) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int blk = wave + 4 * u;
-      const int row = blk * 4 + lane / 16, phys = lane % 16;
-      const int logical = phys ^ (row & 15);
-      const int64_t key = j0 + row < a.Lk ? j0 + row : a.Lk - 1;
-      g2lds16_a(kbase + key * a.skj + logical * 8, kt + blk * 1024);
+      for (int u = 0; u < 4; u++) g2lds16_a(kb + koff[u], kt + (wave + 4 * u) * 1024);
+    } else {
+      // the last tile: rows past the last key re-read it (their scores are masked)
+      const int last = (int)(a.Lk - 1 - j0);
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int krow = (wave + 4 * u) * 4 + lane / 16, kphys = lane % 16;
+        const int r = krow < last ? krow : last;
+        g2lds16_a(kb + ((uint32_t)r * kstride + (uint32_t)((kphys ^ (krow & 15)) << 4)), kt + (wave + 4 * u) * 1024);
+      }
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int blk = wave + 4 * u;
-      const int row = blk * 8 + lane / 8, phys = lane % 8;
-      const int logical = phys ^ ((row >> 1) & 7);
-      g2lds16_a(vbase + row * a.svd + j0 + logical * 8, vt + blk * 1024);
-    }
+    for (int u = 0; u < 4; u++) g2lds16_a(vb + voff[u], vt + (wave + 4 * u) * 1024);
   };
 
-  typedef float v16f_a __attribute__((ext_vector_type(16)));
   v16f_a oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; db++)
 #pragma unroll
     for (int r = 0; r < 16; r++) oacc[db][r] = 0.0f;
-  float m = -__builtin_inff();  // running max of the scaled scores (base-2 units), shared by lanes l, l ^ 32
+  float m = -__builtin_inff();  // reference max of the scaled scores (base-2 units), shared by lanes l, l ^ 32
   float lsum = 0.0f;            // this lane's partial sum of the probabilities
+  const int kswz = l32 & 15, vswz = (l32 >> 1) & 7;   // the lane's rows' swizzles (rows 32 i + l32)
 
   const int64_t nt = (a.Lk + kBK - 1) / kBK;
   issue_tile(0, 0);
@@ -126,77 +154,70 @@ void attention_kernel(const AttnArgs a) {
     const char* vt = kt + kKTile;
     const int64_t j0 = t * kBK;
 
-    // S^T for the tile's two 32-key blocks: lane holds query l32, keys 32 kb + 8 (r / 4) + 4 h2 + r % 4
+    // S^T for the tile's two 32-key blocks (interleaved): lane holds query l32, keys 32 kb + 8 (r / 4) + 4 h2 + r % 4
     v16f_a s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
+    for (int ks = 0; ks < 8; ks++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) s[kb][r] = 0.0f;
-      const int row = 32 * kb + l32;
-#pragma unroll
-      for (int ks = 0; ks < 8; ks++) {
-        const bf16x8 af = *reinterpret_cast<const bf16x8*>(kt + row * 256 + (((2 * ks + h2) ^ (row & 15)) << 4));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], s[kb], 0, 0, 0);
+      for (int kb = 0; kb < 2; kb++) {
+        const bf16x8 af =
+            *reinterpret_cast<const bf16x8*>(kt + (32 * kb + l32) * 256 + (((2 * ks + h2) ^ kswz) << 4));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], ks == 0 ? v16f_a{} : s[kb], 0, 0, 0);
       }
-    }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int64_t key = j0 + 32 * kb + 8 * (r / 4) + 4 * h2 + (r % 4);
-          if (key >= a.Lk) s[kb][r] = -__builtin_inff();
+          const int key = (int)(j0 - a.Lk) + 32 * kb + 8 * (r / 4) + 4 * h2 + (r % 4);
+          if (key >= 0) s[kb][r] = -__builtin_inff();
         }
     }
-    // online softmax: the tile's max for this query (both lanes), the rescale of what came before
+    // online softmax: the tile's max for this query (both lanes), then the lazy move of the reference max
     float mx = s[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) mx = fmax_f(mx, s[kb][r]);
-    mx = fmax_f(mx, __shfl_xor(mx, 32));
-    const float mnew = fmax_f(m, mx * a.scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 0 for the first tile (m = -inf)
-    m = mnew;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+      for (int r = 0; r < 16; r++) mx = __builtin_fmaxf(mx, s[kb][r]);
+    const float mt = max_xor32(mx) * a.scale_log2;
+    const bool grow = mt > m + kSlack;  // always true for the first tile (m = -inf)
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mnew = grow ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 where m stays, 0 for the first tile
+      m = mnew;
       lsum *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; db++)
 #pragma unroll
         for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
     }
-    // probabilities (base-2 exponent of the scaled score minus the max), this lane's sum, bf16 pairs
+    // probabilities (base-2 exponent of the scaled score minus the reference), this lane's sum, bf16 pairs
+    const float nm = -m;
     uint32_t pk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int p = 0; p < 8; p++) {
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p], a.scale_log2, -mnew));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p + 1], a.scale_log2, -mnew));
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p], a.scale_log2, nm));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p + 1], a.scale_log2, nm));
         lsum += e0 + e1;
         pk[kb][p] = bf16x2_finite(e0, e1);
       }
-    // O^T += V^T P^T: step (kb, ks2) takes the 16 keys 32 kb + 16 ks2 + 8 (e / 4) + 4 h2 + e % 4 of element
-    // e of lane half h2, i.e. registers 8 ks2 .. 8 ks2 + 7 of block kb, and the V^T row's keys in the same order
+    // O^T += V^T P^T over the four 16-key groups g = 2 kb + ks2: the B fragment is score registers
+    // 8 ks2 .. 8 ks2 + 7 of block kb, the A fragment chunk 2 g + h2 of each V^T row (the keys in the same order)
 #pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const int row = 32 * db + l32;
-      const int swz = (row >> 1) & 7;
-      const char* vrow = vt + row * 128 + 8 * h2;
+    for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
+      for (int ks2 = 0; ks2 < 2; ks2++) {
+        const v4i_a bi = {(int)pk[kb][4 * ks2], (int)pk[kb][4 * ks2 + 1], (int)pk[kb][4 * ks2 + 2],
+                          (int)pk[kb][4 * ks2 + 3]};
+        const int chunk = (4 * kb + 2 * ks2 + h2) ^ vswz;
 #pragma unroll
-        for (int ks2 = 0; ks2 < 2; ks2++) {
-          const int c0 = 4 * kb + 2 * ks2;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + ((c0 ^ swz) << 4));
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (((c0 + 1) ^ swz) << 4));
-          const v4i_a ai = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
-          const v4i_a bi = {(int)pk[kb][4 * ks2], (int)pk[kb][4 * ks2 + 1], (int)pk[kb][4 * ks2 + 2],
-                            (int)pk[kb][4 * ks2 + 3]};
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ai),
-                                                             __builtin_bit_cast(bf16x8, bi), oacc[db], 0, 0, 0);
+        for (int db = 0; db < 4; db++) {
+          const bf16x8 af = *reinterpret_cast<const bf16x8*>(vt + (32 * db + l32) * 128 + (chunk << 4));
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, bi), oacc[db], 0, 0, 0);
         }
-    }
+      }
   }
   // normalize and store: lane holds query l32, dims 32 db + 8 rr + 4 h2 + 0..3 in registers 4 rr .. 4 rr + 3
   const float ltot = lsum + __shfl_xor(lsum, 32);
@@ -236,6 +257,9 @@ extern "C" int hn_attention(const void* q, int64_t sqb, int64_t sqh, int64_t sqi
   HN_REQUIRE(sqi % 8 == 0 && skj % 8 == 0 && svd % 8 == 0 && sqh % 8 == 0 && skh % 8 == 0 && svh % 8 == 0 &&
                  sqb % 8 == 0 && skb % 8 == 0 && svb % 8 == 0 && soi % 4 == 0 && soh % 4 == 0 && sob % 4 == 0,
              "hn_attention: strides must keep rows 16-byte aligned (out 8-byte)");
+  HN_REQUIRE(skj > 0 && skj <= (1 << 23) && svd > 0 && svd <= (1 << 22),
+             "hn_attention: key stride %lld / V^T row stride %lld out of range (tile offsets are 32-bit)",
+             (long long)skj, (long long)svd);
   HN_REQUIRE(scale > 0.0f && scale < 1e30f, "hn_attention: bad scale");
   if (B == 0 || Lq == 0) return HN_OK;
   const int64_t qblocks = (Lq + kBQ - 1) / kBQ;

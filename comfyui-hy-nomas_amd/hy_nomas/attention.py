@@ -34,14 +34,25 @@ def _hip_ok(q, k, v):
 
 
 def transpose_values(vh):
-    """vh [B, H, Lk, D] -> V^T [B, H, D, Lk_pad] bf16 with the keys contiguous and zero padding up to a multiple of
-    the kernel's key tile (the layout `hn_attention` reads V in)."""
+    """vh [B, H, Lk, D] -> V^T [B, H, D, Lk_pad] bf16: the layout `hn_attention` reads V in.  Keys run along the
+    last dim, padded with zero keys up to a multiple of the kernel's key tile, and the keys of each 16-key group
+    are stored in the order 0-3, 8-11, 4-7, 12-15 (key 16 g + 8 a + 4 b + c at position 16 g + 8 b + 4 a + c),
+    the order in which the kernel's matrix-core operands hold them."""
     b, h, lk, d = vh.shape
     pad = -(-lk // KEY_TILE) * KEY_TILE
     vt = torch.empty((b, h, d, pad), device=vh.device, dtype=torch.bfloat16)
-    if pad > lk:
-        vt[..., lk:].zero_()
-    vt[..., :lk].copy_(vh.transpose(-1, -2))
+    full = lk // 16 * 16
+
+    def put(dst, src):  # src [B, H, n, D] (n % 16 == 0) -> dst [B, H, D, n] in the grouped key order
+        n = src.shape[2]
+        dst.unflatten(3, (n // 16, 2, 2, 4)).copy_(src.unflatten(2, (n // 16, 2, 2, 4)).permute(0, 1, 6, 2, 4, 3, 5))
+
+    if full:
+        put(vt[..., :full], vh[:, :, :full])
+    if pad > full:
+        tail = torch.zeros((b, h, pad - full, d), device=vh.device, dtype=torch.bfloat16)
+        tail[:, :, :lk - full] = vh[:, :, full:]
+        put(vt[..., full:], tail)
     return vt
 
 

@@ -156,8 +156,11 @@ int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, con
  * group's keys.
  *   out[b, i, h, :] = sum_j softmax_j(scale * q[b, i, h, :] . k[b, j, h, :]) v[b, j, h, :]
  * bf16 q, k, out with head dim D == 128 (contiguous), any element strides of batch / head / token;
- * V is given transposed: vt[b, h, d, j] at vt + b svb + h svh + d svd + j, and every V^T row must be readable
- * up to ceil(Lk / 64) * 64 keys with finite values past Lk (svd >= that; zeros are the usual padding).
+ * V is given transposed with the keys of each 16-key group reordered: key j = 16 g + 8 a + 4 b + c
+ * (a, b in {0, 1}, c in 0..3) of dim d at vt + b svb + h svh + d svd + 16 g + 8 b + 4 a + c (the order 0-3,
+ * 8-11, 4-7, 12-15 in each group), and every V^T row must be readable up to ceil(Lk / 64) * 64 positions with
+ * finite values at the positions of keys past Lk (svd >= that; zeros are the usual padding).
+ * 0 < skj <= 2^23 and 0 < svd <= 2^22 elements.
  * fp32 scores and softmax, bf16 probabilities in the second product, bf16 out.  Lk >= 1.
  */
 int hn_attention(const void* q, int64_t sqb, int64_t sqh, int64_t sqi, const void* k, int64_t skb, int64_t skh,

@@ -206,8 +206,8 @@ def test_whole_k_int8_routes_long_k_to_the_group_fold(monkeypatch):
 
 
 def test_attention_backend_selection_and_value_layout(monkeypatch):
-    """The attention backend switch (HY_NOMAS_ATTENTION) and the kernel's V^T layout: keys contiguous, padded
-    with zeros up to the 64-key tile."""
+    """The attention backend switch (HY_NOMAS_ATTENTION) and the kernel's V^T layout: keys along the last dim in
+    the grouped order, padded with zeros up to the 64-key tile."""
     from hy_nomas import attention
 
     monkeypatch.delenv(attention.BACKEND_ENV, raising=False)
@@ -217,10 +217,20 @@ def test_attention_backend_selection_and_value_layout(monkeypatch):
     monkeypatch.setenv(attention.BACKEND_ENV, "flash")
     with pytest.raises(ValueError):
         attention.backend()
-    vh = torch.randn(2, 3, 70, 128).to(torch.bfloat16)
-    vt = attention.transpose_values(vh)
-    assert vt.shape == (2, 3, 128, 128)
-    assert torch.equal(vt[..., :70], vh.transpose(-1, -2)) and not vt[..., 70:].any()
+    for lk in (70, 64, 5, 130):
+        vh = torch.randn(2, 3, lk, 128).to(torch.bfloat16)
+        vt = attention.transpose_values(vh)
+        pad = -(-lk // 64) * 64
+        assert vt.shape == (2, 3, 128, pad)
+        # key j at position 16 (j // 16) + 8 ((j // 4) % 2) + 4 ((j // 8) % 2) + j % 4; the other positions are 0
+        pos = [16 * (j // 16) + 8 * ((j // 4) % 2) + 4 * ((j // 8) % 2) + j % 4 for j in range(lk)]
+        assert len(set(pos)) == lk and max(pos) < pad
+        assert torch.equal(vt[..., pos], vh.transpose(-1, -2))
+        rest = sorted(set(range(pad)) - set(pos))
+        assert not vt[..., rest].any()
+    # a token-major value tensor viewed head-major (the layout attention() passes)
+    v = torch.randn(1, 40, 2, 128).to(torch.bfloat16)
+    assert torch.equal(attention.transpose_values(v.transpose(1, 2)), attention.transpose_values(v.transpose(1, 2).contiguous()))
     k = torch.randn(1, 5, 2, 128)
     hk = torch.randn(1, 3, 2, 128)
     keys, vals = attention._keys([(hk, hk + 1), None, (k, k + 1), (k[:, :0], k[:, :0])])
