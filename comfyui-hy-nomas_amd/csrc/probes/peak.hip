@@ -99,22 +99,10 @@ __global__ __launch_bounds__(kWaves * 64) void mfma_fp8_loop(const v8i* a, const
   }
 }
 
-// Each thread moves 4 x 16 bytes per round (four loads in flight before the stores); whole rounds of the
-// grid first, then the tail one chunk per thread.
+// One 16-byte chunk per thread, one pass of the grid (the caller launches ceil(n / 256) workgroups).
 __global__ __launch_bounds__(256) void copy16(const v4i* __restrict__ src, v4i* __restrict__ dst, int64_t n) {
-  const int64_t threads = (int64_t)gridDim.x * blockDim.x;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t rounds = n / (4 * threads);
-  for (int64_t r = 0; r < rounds; r++) {
-    const int64_t base = r * 4 * threads + t;
-    v4i v[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) v[u] = __builtin_nontemporal_load(src + base + u * threads);
-#pragma unroll
-    for (int u = 0; u < 4; u++) __builtin_nontemporal_store(v[u], dst + base + u * threads);
-  }
-  for (int64_t i = rounds * 4 * threads + t; i < n; i += threads)
-    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
 }  // namespace
@@ -143,9 +131,12 @@ extern "C" int hnp_mfma_loop(int kind, const void* a, const void* b, int iters, 
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
-// dst[0:bytes) = src[0:bytes); bytes % 16 == 0, both 16-byte aligned.
+// dst[0:bytes) = src[0:bytes); bytes % 16 == 0, both 16-byte aligned.  (`blocks` is unused: one thread per chunk.)
 extern "C" int hnp_copy(const void* src, void* dst, int64_t bytes, int blocks, void* stream) {
-  if (!src || !dst || bytes <= 0 || bytes % 16 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15) || blocks <= 0) return 1;
-  hipLaunchKernelGGL(copy16, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const v4i*)src, (v4i*)dst, bytes / 16);
+  (void)blocks;
+  if (!src || !dst || bytes <= 0 || bytes % 16 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15)) return 1;
+  const int64_t n = bytes / 16, grid = (n + 255) / 256;
+  if (grid > 0x7fffffff) return 1;
+  hipLaunchKernelGGL(copy16, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const v4i*)src, (v4i*)dst, n);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
