@@ -1,13 +1,16 @@
 """Attention of the double-stream block on the gfx950 bf16 matrix cores (hy_nomas/model.py:145-223).
 
-`attention(q, k, v)` has the reference's signature and result: q [B, Lq, H, D], k / v [B, Lk, H, D] -> softmax
-attention over all keys, [B, Lq, H, D].  `segment_attention(q, k, v, history, plan)` is the reference's
-segment-level call: the current tokens attend to the cached history keys plus the current video keys and,
-with an action plan, to their own group's text keys.
+`attention(q, k, v, transformer_options=None)` has the reference's signature and result: q [B, Lq, H, D],
+k / v [B, Lk, H, D] -> softmax attention over all keys, [B, Lq, H, D].  `segment_attention(q, k, v, history,
+plan, transformer_options=None)` is the reference's segment-level call: the current tokens attend to the
+cached history keys plus the current video keys and, with an action plan, to their own group's text keys.
+`transformer_options` (ComfyUI's per-call options, which the reference hands to ComfyUI's attention) is
+accepted in the same position and not used.
 
-Two backends: "sdpa" (torch's scaled-dot-product attention, the default the reference also reaches through
-ComfyUI) and "hip" (this package's kernel, `hn_attention`).  `HY_NOMAS_ATTENTION` selects one for every call
-that does not name it.  The HIP kernel takes head dim 128 in bf16; other inputs use SDPA.
+Two backends, chosen by the keyword `backend`: "sdpa" (torch's scaled-dot-product attention, the default the
+reference also reaches through ComfyUI) and "hip" (this package's kernel, `hn_attention`).
+`HY_NOMAS_ATTENTION` selects one for every call that does not name it.  The HIP kernel takes head dim 128 in
+bf16; other inputs use SDPA.
 """
 import os
 
@@ -20,7 +23,7 @@ BACKEND_ENV = "HY_NOMAS_ATTENTION"
 KEY_TILE = 64          # keys per tile of the kernel; V^T rows are padded to a multiple of it
 
 
-def backend(name=None):
+def choose_backend(name=None):
     """The attention backend of a call: `name`, else HY_NOMAS_ATTENTION, else "sdpa"."""
     name = name or os.environ.get(BACKEND_ENV, "sdpa")
     if name not in ("sdpa", "hip"):
@@ -89,18 +92,18 @@ def attention_hip(q, k, vt, lk, out=None, scale=None):
     return out
 
 
-def attention(q, k, v, backend_name=None):
+def attention(q, k, v, transformer_options=None, *, backend=None):
     """q [B, Lq, H, D], k / v [B, Lk, H, D] -> [B, Lq, H, D] (hy_nomas/model.py:145-150)."""
-    if backend(backend_name) == "hip" and _hip_ok(q, k, v):
+    if choose_backend(backend) == "hip" and _hip_ok(q, k, v):
         vt = transpose_values(v.transpose(1, 2))
         return attention_hip(q, k, vt, k.shape[1])
     return sdpa(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)).transpose(1, 2)
 
 
-def attention_heads(qh, kh, vh, backend_name=None):
+def attention_heads(qh, kh, vh, backend=None):
     """`attention` on head-major operands qh [B, H, Lq, D], kh / vh [B, H, Lk, D] (as the QKV epilogue writes
     them).  Returns [B, Lq, H, D] (a view for SDPA, a contiguous tensor for the HIP kernel)."""
-    if backend(backend_name) == "hip" and _hip_ok(qh, kh, vh):
+    if choose_backend(backend) == "hip" and _hip_ok(qh, kh, vh):
         return attention_hip(qh.transpose(1, 2), kh.transpose(1, 2), transpose_values(vh), kh.shape[2])
     return sdpa(qh, kh, vh).transpose(1, 2)
 
@@ -124,7 +127,7 @@ def _keys(parts):
     return torch.cat([p[0] for p in parts], dim=1), torch.cat([p[1] for p in parts], dim=1)
 
 
-def segment_attention(q, k, v, history, plan, backend_name=None):
+def segment_attention(q, k, v, history, plan, transformer_options=None, *, backend=None):
     """The current tokens' attention of one segment (hy_nomas/model.py:199-223): q / k / v [B, Lv + Lt, H, D] (video
     tokens first), history (hk, hv) [1 or B, Lh, H, D] or None, plan with `groups` (None: every current token
     queries every key) and `video_tokens`.  Each group's queries attend to the history, every current video key
@@ -135,11 +138,11 @@ def segment_attention(q, k, v, history, plan, backend_name=None):
         hist = tuple(t if t.shape[0] == batch else t.expand(batch, -1, -1, -1) for t in history)
     groups = getattr(plan, "groups", None)
     if groups is None:
-        return attention(q, *_keys([hist, (k, v)]), backend_name)
+        return attention(q, *_keys([hist, (k, v)]), backend=backend)
     lv = plan.video_tokens
     video = (k[:, :lv], v[:, :lv])
     out = torch.empty_like(q)
     for q_idx, text_idx in groups:
         text = (k[:, lv + text_idx], v[:, lv + text_idx]) if text_idx.numel() else None
-        out[:, q_idx] = attention(q[:, q_idx], *_keys([hist, video, text]), backend_name)
+        out[:, q_idx] = attention(q[:, q_idx], *_keys([hist, video, text]), backend=backend)
     return out

@@ -32,11 +32,11 @@ def test_attention_matches_float32(dev, b, h, lq, lk, mag):
     q = (torch.randn(b, lq, h, 128, generator=g) * mag).to(torch.bfloat16).to(dev)
     k = (torch.randn(b, lk, h, 128, generator=g) * mag).to(torch.bfloat16).to(dev)
     v = torch.randn(b, lk, h, 128, generator=g).to(torch.bfloat16).to(dev)
-    got = attention.attention(q, k, v, "hip")
+    got = attention.attention(q, k, v, backend="hip")
     assert got.shape == (b, lq, h, 128) and got.dtype == torch.bfloat16 and torch.isfinite(got.float()).all()
     fro, mx = rel(got, ref_attention(q, k, v))
     assert fro < 1e-2 and mx < 3e-2, (fro, mx)
-    fro_s, _ = rel(got, attention.attention(q, k, v, "sdpa"))
+    fro_s, _ = rel(got, attention.attention(q, k, v, backend="sdpa"))
     assert fro_s < 1e-2, fro_s
 
 
@@ -46,7 +46,7 @@ def test_attention_heads_on_strided_qkv(dev):
 
     g = seeded(12)
     hm = torch.randn(3, 2, 4, 333, 128, generator=g).to(torch.bfloat16).to(dev)
-    got = attention.attention_heads(hm[0], hm[1], hm[2], "hip")
+    got = attention.attention_heads(hm[0], hm[1], hm[2], backend="hip")
     ref = ref_attention(*(t.transpose(1, 2) for t in hm))
     assert got.shape == (2, 333, 4, 128)
     fro, mx = rel(got, ref)
@@ -62,7 +62,7 @@ def test_attention_full_config4_length(dev):
     gen = torch.Generator(device=dev).manual_seed(5)
     L, H = 57600, 24
     hm = torch.randn(3, 1, H, L, 128, generator=gen, device=dev).to(torch.bfloat16)
-    got = attention.attention_heads(hm[0], hm[1], hm[2], "hip")
+    got = attention.attention_heads(hm[0], hm[1], hm[2], backend="hip")
     rows = torch.tensor(sorted(set(torch.randperm(L, generator=seeded(6))[:48].tolist() + [0, L - 1])), device=dev)
     qh, kh, vh = (t[0].float() for t in hm)                       # [H, L, 128]
     s = torch.matmul(qh[:, rows], kh.transpose(-1, -2).contiguous()) * 128 ** -0.5
@@ -89,7 +89,7 @@ def test_segment_attention_history_and_groups(dev):
     groups = [(torch.cat([torch.arange(0, 90), torch.arange(lv, lv + 10)]).to(dev), torch.arange(0, 10).to(dev)),
               (torch.cat([torch.arange(90, lv), torch.arange(lv + 10, lv + lt)]).to(dev), torch.arange(10, 40).to(dev))]
     for plan in (Plan(lv, None), Plan(lv, groups)):
-        got = attention.segment_attention(q, k, v, (hk, hv), plan, "hip")
+        got = attention.segment_attention(q, k, v, (hk, hv), plan, None, backend="hip")
         ref = torch.empty(b, lv + lt, h, 128, device=dev)
         for q_idx, t_idx in (plan.groups or [(torch.arange(lv + lt, device=dev), torch.arange(lt, device=dev))]):
             keys = torch.cat([hk, k[:, :lv], k[:, lv + t_idx]], dim=1)
@@ -97,7 +97,7 @@ def test_segment_attention_history_and_groups(dev):
             ref[:, q_idx] = ref_attention(q[:, q_idx], keys, vals)
         fro, mx = rel(got, ref)
         assert fro < 1e-2 and mx < 3e-2, (plan.groups is None, fro, mx)
-        fro_s, _ = rel(got, attention.segment_attention(q, k, v, (hk, hv), plan, "sdpa"))
+        fro_s, _ = rel(got, attention.segment_attention(q, k, v, (hk, hv), plan, {}, backend="sdpa"))
         assert fro_s < 1e-2
 
 

@@ -211,12 +211,12 @@ def test_attention_backend_selection_and_value_layout(monkeypatch):
     from hy_nomas import attention
 
     monkeypatch.delenv(attention.BACKEND_ENV, raising=False)
-    assert attention.backend() == "sdpa" and attention.backend("hip") == "hip"
+    assert attention.choose_backend() == "sdpa" and attention.choose_backend("hip") == "hip"
     monkeypatch.setenv(attention.BACKEND_ENV, "hip")
-    assert attention.backend() == "hip" and attention.backend("sdpa") == "sdpa"
+    assert attention.choose_backend() == "hip" and attention.choose_backend("sdpa") == "sdpa"
     monkeypatch.setenv(attention.BACKEND_ENV, "flash")
     with pytest.raises(ValueError):
-        attention.backend()
+        attention.choose_backend()
     for lk in (70, 64, 5, 130):
         vh = torch.randn(2, 3, lk, 128).to(torch.bfloat16)
         vt = attention.transpose_values(vh)
@@ -235,3 +235,43 @@ def test_attention_backend_selection_and_value_layout(monkeypatch):
     hk = torch.randn(1, 3, 2, 128)
     keys, vals = attention._keys([(hk, hk + 1), None, (k, k + 1), (k[:, :0], k[:, :0])])
     assert torch.equal(keys, torch.cat([hk, k], dim=1)) and torch.equal(vals, torch.cat([hk + 1, k + 1], dim=1))
+
+
+def test_attention_reference_signature_and_segments_cpu():
+    """attention / segment_attention called as the reference's model.py calls them (transformer_options in the
+    4th / 6th position), on float32 CPU tensors (the SDPA backend), against explicit softmax attention: every
+    query group attends to [history | all current video keys | its own text keys] (model.py:199-223)."""
+    from hy_nomas import attention
+
+    g = torch.Generator().manual_seed(31)
+    b, h, lv, lt, lh, d = 2, 2, 30, 12, 9, 128
+    q, k, v = (torch.randn(b, lv + lt, h, d, generator=g) for _ in range(3))
+    hk, hv = (torch.randn(1, lh, h, d, generator=g) for _ in range(2))
+
+    def softmax_attn(qq, kk, vv):
+        s = torch.einsum("bqhd,bkhd->bhqk", qq, kk) / d ** 0.5
+        return torch.einsum("bhqk,bkhd->bqhd", torch.softmax(s, dim=-1), vv)
+
+    out = attention.attention(q, k, v, {"patches": {}})
+    assert torch.allclose(out, softmax_attn(q, k, v), atol=1e-5)
+
+    class Plan:
+        video_tokens = lv
+        groups = [(torch.cat([torch.arange(0, 20), torch.arange(lv, lv + 5)]), torch.arange(0, 5)),
+                  (torch.cat([torch.arange(20, lv), torch.arange(lv + 5, lv + lt)]), torch.tensor([0, 5, 6, 7, 8, 9, 10, 11])),
+                  ]
+
+    got = attention.segment_attention(q, k, v, (hk, hv), Plan(), {})
+    want = torch.empty_like(q)
+    for q_idx, t_idx in Plan.groups:
+        keys = torch.cat([hk.expand(b, -1, -1, -1), k[:, :lv], k[:, lv + t_idx]], dim=1)
+        vals = torch.cat([hv.expand(b, -1, -1, -1), v[:, :lv], v[:, lv + t_idx]], dim=1)
+        want[:, q_idx] = softmax_attn(q[:, q_idx], keys, vals)
+    assert torch.allclose(got, want, atol=1e-5)
+
+    class NoGroups:
+        video_tokens = lv
+        groups = None
+
+    got = attention.segment_attention(q, k, v, None, NoGroups(), None)
+    assert torch.allclose(got, softmax_attn(q, k, v), atol=1e-5)
