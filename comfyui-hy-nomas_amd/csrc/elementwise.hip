@@ -81,6 +81,11 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
   for (int i = 0; i < CPL; i++)
     if (has(i)) xv[i] = ld_nt16(x + r * D + (lane + 64 * i) * 8);
+  // the row's outputs: chunk i of this lane at a fixed offset from one per-row base (512 codes / 1 KB of
+  // 2-byte outputs / 4 group scales further per chunk), so the stores take immediate offsets
+  uint16_t* const yrow = QUANT ? nullptr : y + r * D + lane * 8;
+  int8_t* const qrow = QUANT ? q + r * D + lane * 8 : nullptr;
+  float* const srow = QUANT && !PT ? s + r * (D / 128) + (lane >> 4) : nullptr;
 
   int fin = 1;
   for (int c = threadIdx.x; c < nchunk; c += kRowThreads) {
@@ -182,7 +187,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(f[i][j] / gs);
         }
-        st_nt8(q + r * D + c * 8, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
+        st_nt8(qrow + 512 * i, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
       }
     }
     if (lane == 0) s[r] = gs;
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
       }
       if constexpr (!QUANT) {
         const uint4 packed = finite ? narrow8x<DT, true>(o) : narrow8x<DT, false>(o);
-        st_nt16(y + r * D + c * 8, packed);
+        st_nt16(yrow + 512 * i, packed);
       } else {
         float peak = 0.0f;
         if (__builtin_expect(finite, 1) && DT == HN_DTYPE_BF16) {
@@ -236,9 +241,9 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(o[j] / gs);
         }
-        st_nt8(q + r * D + c * 8, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
+        st_nt8(qrow + 512 * i, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
         // all 16 lanes of the group store the same scale to the same address (no divergent branch)
-        s[r * (D / 128) + c / 16] = gs;
+        srow[4 * i] = gs;
       }
     }
   }
