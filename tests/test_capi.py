@@ -81,3 +81,25 @@ def test_argument_validation_without_a_gpu():
     rc = l.hn_block_gemm(None, 131072, None, 1024, None, 131072, None, 1024, 1, None, 0, 4, 8, 131072, 128, 0, 3,
                          None, 0, 8, None, 0, None)   # ACC32 always sums the whole K in int32
     assert rc == 1 and b"overflow" in l.hn_last_error()
+
+
+def test_attention_argument_validation_without_a_gpu():
+    """hn_attention rejects, on the host: a head dim other than 128, V^T rows shorter than the key tiles, strides
+    past the 32-bit tile offsets, and a non-positive scale (non-null, 16-byte aligned dummy pointers that are
+    never dereferenced, since every case fails before a launch)."""
+    import torch  # noqa: F401
+    from hy_nomas import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhynomas_hip.so not built")
+    l = _lib.lib()
+    p = 4096  # a 16-byte aligned address the checks never read
+
+    def call(D=128, svd=128, skj=128, scale=0.088, Lk=100):
+        return l.hn_attention(p, 0, 0, 128, p, 0, 0, skj, p, 0, 0, svd, p, 0, 0, 128, 1, 1, 10, Lk, D, scale, None)
+
+    assert call(D=96) == 1 and b"head dim" in l.hn_last_error()
+    assert call(svd=64) == 1 and b"V^T rows" in l.hn_last_error()
+    assert call(skj=1 << 24) == 1 and b"out of range" in l.hn_last_error()
+    assert call(scale=0.0) == 1 and b"scale" in l.hn_last_error()
+    assert call(Lk=0) == 1 and b"bad shape" in l.hn_last_error()
