@@ -83,8 +83,14 @@ class DoubleStreamBlockInt8:
     def __init__(self, img, txt):
         self.img, self.txt = img, txt
 
-    def forward(self, img, txt, img_mods, txt_mods, rope=None, backend=None):
-        """`backend`: the attention backend ("sdpa", "hip"; None: HY_NOMAS_ATTENTION, else "sdpa")."""
+    def forward(self, img, txt, img_mods, txt_mods, rope=None, backend=None, history=None, plan=None,
+                capture=None):
+        """`backend`: the attention backend ("sdpa", "hip"; None: HY_NOMAS_ATTENTION, else "sdpa").
+        As the reference's block (hy_nomas/model.py:288-297): `history` is the cached (keys, values) of earlier
+        segments, [1 or B, Lh, H, D], or None; `plan` the segment's attention plan (`groups`, `video_tokens`;
+        model.py:154-196), or None for every current token attending to every key; `capture(k, v)` is called
+        with the current tokens' keys and values [B, L, H, D] (views of the QKV buffer), as the reference hands
+        them to the history cache."""
         shift1, scale1, gate1, shift2, scale2, gate2 = img_mods
         tshift1, tscale1, tgate1, tshift2, tscale2, tgate2 = txt_mods
         b, lv = img.shape[0], img.shape[1]
@@ -94,7 +100,13 @@ class DoubleStreamBlockInt8:
                          device=img.device, dtype=torch.bfloat16)
         self.img.attention_heads(img, shift1, scale1, rope, out=hm, l_offset=0)
         self.txt.attention_heads(txt, tshift1, tscale1, None, out=hm, l_offset=lv)
-        out = attn.attention_heads(hm[0], hm[1], hm[2], backend)
+        if capture is not None:
+            capture(hm[1].transpose(1, 2), hm[2].transpose(1, 2))
+        if history is None and getattr(plan, "groups", None) is None:
+            out = attn.attention_heads(hm[0], hm[1], hm[2], backend)
+        else:
+            q, k, v = (t.transpose(1, 2) for t in hm)
+            out = attn.segment_attention(q, k, v, history, plan, backend=backend)
         del hm
         out = out.reshape(b, out.shape[1], -1)
         img = self.img.post(img, out[:, :lv], gate1, shift2, scale2, gate2)

@@ -98,17 +98,51 @@ def _post(blk, x, attn, mods, eps):
     return x + _linear(h, blk.fc2) * gate2.unsqueeze(1)
 
 
-def reference_double_stream(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope=None, eps=1e-6):
+def softmax_attention(q, k, v):
+    """float32 softmax(q k^T / sqrt(D)) v on token-major q [B, Lq, H, D], k / v [B, Lk, H, D] -> [B, Lq, H, D]."""
+    qh, kh, vh = (t.float().transpose(1, 2) for t in (q, k, v))
+    p = torch.softmax(qh @ kh.transpose(-1, -2).contiguous() / qh.shape[-1] ** 0.5, dim=-1)
+    return (p @ vh.contiguous()).transpose(1, 2)
+
+
+def segment_attention(q, k, v, history=None, groups=None, video_tokens=None):
+    """The segment's attention of hy_nomas/model.py:199-223 in float32: q / k / v [B, Lv + Lt, H, D] are the
+    current tokens (video first); history (hk, hv) [1 or B, Lh, H, D] or None.  Without groups every current
+    token attends to [history | all current keys]; with groups [(query indices, text key indices)] each group's
+    queries attend to [history | the current video keys | the group's text keys]."""
+    b = q.shape[0]
+    hist = None
+    if history is not None:
+        hist = tuple(t.float().expand(b, -1, -1, -1) for t in history)
+    if groups is None:
+        keys = k if hist is None else torch.cat([hist[0], k.float()], dim=1)
+        vals = v if hist is None else torch.cat([hist[1], v.float()], dim=1)
+        return softmax_attention(q, keys, vals)
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    for q_idx, t_idx in groups:
+        ks, vs = [k[:, :video_tokens].float()], [v[:, :video_tokens].float()]
+        if hist is not None:
+            ks.insert(0, hist[0])
+            vs.insert(0, hist[1])
+        if t_idx.numel():
+            ks.append(k[:, video_tokens + t_idx].float())
+            vs.append(v[:, video_tokens + t_idx].float())
+        out[:, q_idx] = softmax_attention(q[:, q_idx], torch.cat(ks, dim=1), torch.cat(vs, dim=1))
+    return out
+
+
+def reference_double_stream(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope=None, eps=1e-6, history=None,
+                            groups=None):
     """The double-stream block in float32 torch arithmetic with dequantized weights and unquantized
     activations (the reference's exact-matmul path).  img_blk / txt_blk carry `qkv, proj, fc1, fc2` (int8 codes
-    `qw`, scales `sw`, `bias`), `q_norm_w`, `k_norm_w`, `heads`.  Returns (img, txt) float32."""
+    `qw`, scales `sw`, `bias`), `q_norm_w`, `k_norm_w`, `heads`.  history / groups: as `segment_attention`.
+    Returns (img, txt) float32."""
     img, txt = img.float(), txt.float()
     iq, ik, iv = _qkv(img_blk, img, img_mods, rope, eps)
     tq, tk, tv = _qkv(txt_blk, txt, txt_mods, None, eps)
-    q, k, v = (torch.cat(p, dim=1).transpose(1, 2) for p in ((iq, tq), (ik, tk), (iv, tv)))
-    att = torch.softmax(q @ k.transpose(-1, -2) / q.shape[-1] ** 0.5, dim=-1) @ v
-    att = att.transpose(1, 2).reshape(img.shape[0], -1, img.shape[2])
+    q, k, v = (torch.cat(p, dim=1) for p in ((iq, tq), (ik, tk), (iv, tv)))
     lv = img.shape[1]
+    att = segment_attention(q, k, v, history, groups, lv).reshape(img.shape[0], -1, img.shape[2])
     return _post(img_blk, img, att[:, :lv], img_mods, eps), _post(txt_blk, txt, att[:, lv:], txt_mods, eps)
 
 

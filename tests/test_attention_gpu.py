@@ -125,3 +125,51 @@ def test_double_stream_block_on_the_hip_backend(dev, per_token):
     for got, sd, ref in ((gi, si, ri), (gt, st, rt)):
         assert rel(got, ref)[0] < 2e-2
         assert rel(got, sd)[0] < 1e-2
+
+
+@pytest.mark.parametrize("backend", ["hip", "sdpa"])
+def test_double_stream_block_with_history_plan_and_capture(dev, backend):
+    """The block's attention with the reference's segment inputs (hy_nomas/model.py:288-297): cached history keys
+    and values, an action plan's query groups, and the capture hook, against the float32 block with the same
+    segment attention; the captured keys / values are the QKV epilogue's own."""
+    from hy_nomas import block
+    from oracle import torch_forms
+    from test_block_gpu import make_stream
+
+    d, heads, mlp, lv, lt, lh = 256, 2, 1024, 200, 40, 64
+    g = seeded(217)
+    img_blk = make_stream(d, heads, mlp, g, False, dev)
+    txt_blk = make_stream(d, heads, mlp, g, False, dev)
+    img = torch.randn(1, lv, d, generator=g).to(torch.bfloat16).to(dev)
+    txt = torch.randn(1, lt, d, generator=g).to(torch.bfloat16).to(dev)
+    img_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
+    txt_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
+    rope = [t.to(dev) for t in torch_forms.rope_freqs([32, 48, 48], 256, 2, 10, 10)]
+    history = tuple(torch.randn(1, lh, heads, d // heads, generator=g).to(torch.bfloat16).to(dev) for _ in range(2))
+    groups = [(torch.cat([torch.arange(0, 120), torch.arange(lv, lv + 15)]).to(dev), torch.arange(0, 15).to(dev)),
+              (torch.cat([torch.arange(120, lv), torch.arange(lv + 15, lv + lt)]).to(dev),
+               torch.cat([torch.arange(0, 5), torch.arange(15, lt)]).to(dev))]
+
+    class Plan:
+        video_tokens = lv
+
+    plan = Plan()
+    plan.groups = groups
+    captured = []
+    blk = block.DoubleStreamBlockInt8(img_blk, txt_blk)
+    with torch.no_grad():
+        for hist, pl in ((history, None), (None, plan), (history, plan)):
+            captured.clear()
+            gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope, backend, history=hist, plan=pl,
+                                 capture=lambda k, v: captured.append((k.clone(), v.clone())))
+            ri, rt = torch_forms.reference_double_stream(img_blk, txt_blk, img, txt, img_mods, txt_mods, rope,
+                                                         history=hist, groups=pl.groups if pl else None)
+            for got, ref in ((gi, ri), (gt, rt)):
+                assert rel(got, ref)[0] < 2e-2, (hist is None, pl is None, rel(got, ref))
+            (ck, cv), = captured
+            assert ck.shape == (1, lv + lt, heads, d // heads) and cv.shape == ck.shape
+    # the captured keys / values (image tokens first) against the float32 block's own q / k / v of each stream
+    _, rki, rvi = torch_forms._qkv(img_blk, img.float(), img_mods, rope, 1e-6)
+    _, rkt, rvt = torch_forms._qkv(txt_blk, txt.float(), txt_mods, None, 1e-6)
+    assert rel(ck, torch.cat([rki, rkt], dim=1))[0] < 1e-2
+    assert rel(cv, torch.cat([rvi, rvt], dim=1))[0] < 1e-2

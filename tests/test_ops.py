@@ -275,3 +275,9 @@ def test_attention_reference_signature_and_segments_cpu():
 
     got = attention.segment_attention(q, k, v, None, NoGroups(), None)
     assert torch.allclose(got, softmax_attn(q, k, v), atol=1e-5)
+    # the float32 form the block tests compare with agrees (with and without history, with and without groups)
+    from oracle import torch_forms
+    for hist in (None, (hk, hv)):
+        for plan in (NoGroups(), Plan()):
+            assert torch.allclose(torch_forms.segment_attention(q, k, v, hist, plan.groups, lv),
+                                  attention.segment_attention(q, k, v, hist, plan, {}), atol=1e-5)
