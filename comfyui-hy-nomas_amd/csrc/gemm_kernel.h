@@ -731,15 +731,23 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
               for (int rr = 0; rr < 4; rr++) {
                 const int nl = (tl >> 5) * 4 + i * 32 + rr * 8;
-                int c[4];
+                float y[4];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                   const float v = MF::get(acc[i][J0 + jj], rr * 4 + q);
-                  const float y = __builtin_expect(fast, 1) ? div(v) : v / gs;
-                  if constexpr (KIND == HN_KIND_FP8) c[q] = (int)e4m3_encode(y);
-                  else c[q] = round_half_away_i8(y);
+                  y[q] = __builtin_expect(fast, 1) ? div(v) : v / gs;
                 }
-                *reinterpret_cast<uint32_t*>(o + (uint32_t)(ml * (int)a.ldo + nl)) = pack4_i8(c[0], c[1], c[2], c[3]);
+                uint32_t w;
+                if constexpr (KIND == HN_KIND_FP8) {
+                  // fast groups: finite quotients, the hardware conversion; others the software encoder
+                  w = __builtin_expect(fast, 1) ? e4m3_pack4_hw(y[0], y[1], y[2], y[3])
+                                                : pack4_i8(e4m3_encode(y[0]), e4m3_encode(y[1]), e4m3_encode(y[2]),
+                                                           e4m3_encode(y[3]));
+                } else {
+                  w = pack4_i8(round_half_away_i8(y[0]), round_half_away_i8(y[1]), round_half_away_i8(y[2]),
+                               round_half_away_i8(y[3]));
+                }
+                *reinterpret_cast<uint32_t*>(o + (uint32_t)(ml * (int)a.ldo + nl)) = w;
               }
             if (tl < 32) a.qs[(em0 + ml) * a.ldqs + en0 / 256] = gs;
           }

@@ -65,6 +65,15 @@ __device__ __forceinline__ uint32_t e4m3_encode(float f) {
   return sign | code;
 }
 
+// Four e4m3 codes, low byte first, by the hardware conversion (v_cvt_pk_fp8_f32: OCP e4m3fn, round to nearest
+// even).  It equals e4m3_encode for every finite |x| < 2^9 of either sign (an exhaustive check on the GPU over
+// all such fp32 values, both byte positions and both half-words); the kernels use it only for the finite
+// quotients x / scale of a fast group, which lie within 448 (1 + 2^-22).
+__device__ __forceinline__ uint32_t e4m3_pack4_hw(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 // ----------------------------------------------------------------------------------------------
 // quantization arithmetic
 

@@ -37,13 +37,18 @@ struct Chunk8 {
 template <int KIND, int ROUND, bool FAST>
 __device__ __forceinline__ uint2 encode8(const float* f, float scale) {
   int c[8];
-  if constexpr (FAST) {
+  if constexpr (FAST && KIND == HN_KIND_FP8) {
+    const typename FastQuot<KIND>::Div div(scale);
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) y[i] = div(f[i]);
+    return make_uint2(e4m3_pack4_hw(y[0], y[1], y[2], y[3]), e4m3_pack4_hw(y[4], y[5], y[6], y[7]));
+  } else if constexpr (FAST) {
     const typename FastQuot<KIND>::Div div(scale);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float y = div(f[i]);
-      if constexpr (KIND == HN_KIND_FP8) c[i] = (int)e4m3_encode(y);
-      else if constexpr (ROUND == HN_ROUND_HALF_EVEN) c[i] = (int)__builtin_rintf(y);
+      if constexpr (ROUND == HN_ROUND_HALF_EVEN) c[i] = (int)__builtin_rintf(y);
       else c[i] = round_half_away_i8_inrange(y);
     }
   } else {

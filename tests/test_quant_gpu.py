@@ -119,3 +119,29 @@ def test_fp8_encoding_every_bf16(dev):
     assert torch.all(s.cpu() == 1.0)
     ref = x.float().to(torch.float8_e4m3fn).view(torch.uint8)
     assert torch.equal(q.cpu().view(torch.uint8), ref)
+
+
+def test_hardware_e4m3_conversion_equals_the_encoder(dev):
+    """The hardware OCP e4m3 conversion (v_cvt_pk_fp8_f32) against the software encoder, which the CPU tests pin
+    to torch's float8_e4m3fn cast: every fp32 value with |x| < 2^9 (the quotients x / scale of the fp8
+    quantizers lie within 448 (1 + 2^-22)), both signs, both byte positions and both half-words of the packed
+    result (libhynomas_probes.so: hnp_e4m3_mismatches).  The kernels use the hardware form only for such
+    finite quotients."""
+    import ctypes
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "..", "comfyui-hy-nomas_amd", "hy_nomas", "libhynomas_probes.so")
+    lib = ctypes.CDLL(path)
+    u32, ci, vp = ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p
+    lib.hnp_e4m3_mismatches.argtypes = [u32, u32, ci, vp, vp, vp]
+    blocks = 2048
+    count = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    first = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    hi = 0x44000000  # 2^9
+    print(f"e4m3 conversion over fp32 patterns [0, {hi:#x}) and their negatives", flush=True)
+    assert lib.hnp_e4m3_mismatches(0, hi, blocks, count.data_ptr(), first.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    bad = int(count.sum().item())
+    low = int(first.cpu().numpy().view(np.uint32).min())
+    assert bad == 0, (bad, hex(low))
