@@ -62,7 +62,7 @@ static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
     if constexpr (KIND == HN_KIND_INT8) {  // (fp8 block scales took the branch above)
       if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2, true>(a, st);
     }
-    return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2>(a, st);
+    return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
   }
   set_error("hn_block_gemm: swiglu_quant needs per-token scales or fp8 with 128 x 128 block weight scales");
   return HN_ERR_UNSUPPORTED;

@@ -172,6 +172,22 @@ __device__ __forceinline__ void fold_row_bcast(v16f& facc, const Acc& part, floa
                                                std::integer_sequence<int, R...>) {
   ((facc[R] = fmac_row_bcast<R>(facc[R], w16, (float)part[R] * sa)), ...);
 }
+// registers R0 .. R0 + RN - 1 of the same fold
+template <int R0, typename Acc, int... R>
+__device__ __forceinline__ void fold_rows_bcast(v16f& facc, const Acc& part, float sa, float w16,
+                                                std::integer_sequence<int, R...>) {
+  ((facc[R0 + R] = fmac_row_bcast<R0 + R>(facc[R0 + R], w16, (float)part[R0 + R] * sa)), ...);
+}
+
+// f(std::integral_constant<int, I>()) for I = 0 .. N - 1, in order
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>());
+}
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -348,17 +364,22 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     }
   };
-  auto issue_stage = [&](int kt, int buf) {
+  // load q (0 <= q < LOADS) of stage kt: weight rows, then activation rows, then scales
+  auto issue_load = [&](int kt, int buf, int q) __attribute__((always_inline)) {
     char* base = smem + SCR + buf * STAGE;
-    const uint8_t* wk = wbase + (int64_t)kt * BK;
-    const uint8_t* ak = abase + (int64_t)kt * BK;
-#pragma unroll
-    for (int u = 0; u < A_KB; u++) g2lds16(wk + woff[u], base + (wave + NW * u) * 1024);
-#pragma unroll
-    for (int u = 0; u < B_KB; u++) g2lds16(ak + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
-#pragma unroll
-    for (int u = 0; u < SC_PER_WAVE; u++)
+    if (q < A_KB) {
+      g2lds16(wbase + (int64_t)kt * BK + woff[q], base + (wave + NW * q) * 1024);
+    } else if (q < A_KB + B_KB) {
+      const int u = q - A_KB;
+      g2lds16(abase + (int64_t)kt * BK + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
+    } else {
+      const int u = q - A_KB - B_KB;
       g2lds4(scbase[u] + kt / STAGES_PER_GROUP + scoff[u], smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
+    }
+  };
+  auto issue_stage = [&](int kt, int buf) {
+#pragma unroll
+    for (int q = 0; q < LOADS; q++) issue_load(kt, buf, q);
   };
 
 
@@ -375,6 +396,18 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TM; j++) fb[set][j] = MF::template load<BK>(stage_base + A_BYTES, wrow_m + j * 32, slice, lane);
   };
+
+  // Block-major g128 loop (BMAJ: a separate fp32 running sum, one group per stage).  A wave multiplies its
+  // TN x TM 32x32 blocks one after another (channel block i outer, token block j inner), each through all the
+  // stage's slices, so a block's group partial is complete after SLICES products.  Its fold is issued
+  // between the products of the next block, which accumulate into the second of two partial register sets:
+  // the matrix core works on one block while the VALU folds the previous one.  The stage's last block is
+  // folded during the next stage's first block (and after the tile's last stage).  The activation fragments
+  // of every token block and slice are read once per stage and stay in registers; the weight fragments of
+  // channel block i + 1 replace those of block i slice by slice during block i's last token block.
+  constexpr bool BMAJ = G128 && !RESCALE && !WBLK && STAGES_PER_GROUP == 1;
+  static_assert(!BMAJ || TM >= 2, "the weight fragments of the next channel block are read during the last token block");
+  Frag fbs[BMAJ ? TM : 1][BMAJ ? SLICES : 1], fas[BMAJ ? SLICES : 1];
 
   int64_t m0, n0;
   tile_origin(t, m0, n0);
@@ -447,7 +480,16 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     }
     if (1 < nk) issue_stage(1, 1);
-    read_frags(0, smem + SCR, 0);
+    if constexpr (BMAJ) {
+#pragma unroll
+      for (int j = 0; j < TM; j++)
+#pragma unroll
+        for (int s = 0; s < SLICES; s++) fbs[j][s] = MF::template load<BK>(smem + SCR + A_BYTES, wrow_m + j * 32, s, lane);
+#pragma unroll
+      for (int s = 0; s < SLICES; s++) fas[s] = MF::template load<BK>(smem + SCR, wrow_n, s, lane);
+    } else {
+      read_frags(0, smem + SCR, 0);
+    }
 
     // products of weight fragments [i0, i1) with every activation fragment of register set `set`
     // rs (RESCALE, a stage's first slice): each accumulator block is moved to this group's scale product
@@ -598,13 +640,117 @@ void block_gemm_kernel(const GemmArgs a) {
         }
       }
     };
-    int kt = 0;
-    for (; kt + 2 < nk; kt++) stage_body(kt, kt & 1, std::integral_constant<int, 0>());
-    if (kt + 1 < nk) {
-      stage_body(kt, kt & 1, std::integral_constant<int, 1>());
-      kt++;
+    // BMAJ state: the group partials of two consecutive blocks, and the fold scales of the current group:
+    // per token block the lane's token scale (times the wave's weight scale with block weight scales) and,
+    // per channel block, the lane's DPP source of the per-channel scales.  The tile's first stage folds the
+    // zero partial of "the previous group's last block" with zero scales, which leaves the running sum +0.
+    Acc part[BMAJ ? 2 : 1];
+    float c_sa[TM], c_sw[TN];
+#pragma unroll
+    for (int j = 0; j < TM; j++) c_sa[j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TN; i++) c_sw[i] = 0.0f;
+    auto read_scales = [&](int kt) __attribute__((always_inline)) {
+      const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
+#pragma unroll
+      for (int j = 0; j < TM; j++) {
+        const float sam = sc[BN + wrow_m + j * 32];
+        c_sa[j] = WBLK ? sam * sc[wn * TN * 32] : sam;
+      }
+      if constexpr (!WBLK) {
+        // lane (row R = l >> 4, s = l & 15) holds the scale of channel 32 i + 8 (s >> 2) + 4 (R >> 1) + (s & 3),
+        // which register s of every lane in its row needs (read with a DPP row broadcast)
+#pragma unroll
+        for (int i = 0; i < TN; i++)
+          c_sw[i] = sc[wn * TN * 32 + i * 32 + ((lane & 15) >> 2) * 8 + (lane >> 5) * 4 + (lane & 3)];
+      }
+    };
+    if constexpr (BMAJ) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) part[1][r] = 0;
     }
-    stage_body(kt, kt & 1, std::integral_constant<int, 2>());
+    // outputs [R0, R0 + RN) of one block's fold: facc = fma(float(p) * sa, sw, facc), or with block weight
+    // scales facc = fma(float(p), sa * sw_block, facc)
+    auto fold_chunk = [&](v16f& f, const Acc& p, float fsa, float fsw, auto r0_c, auto rn_c) __attribute__((always_inline)) {
+      constexpr int R0 = decltype(r0_c)::value, RN = decltype(rn_c)::value;
+      if constexpr (WBLK) {
+#pragma unroll
+        for (int r = R0; r < R0 + RN; r++) f[r] = __builtin_fmaf(MF::to_f32(p[r]), fsa, f[r]);
+      } else {
+        fold_rows_bcast<R0>(f, p, fsa, fsw, std::make_integer_sequence<int, RN>());
+      }
+    };
+    constexpr int NB = TN * TM;            // blocks per wave, channel block outer
+    constexpr int FOLD_PER = 16 / SLICES;  // outputs folded after each product
+    constexpr int LAST = (TN - 1) * TM;    // first block of the last channel block
+    // One stage.  The compiler waits for all outstanding LDS reads (lgkmcnt 0) before a product whose
+    // fragments are pending, so reads are issued as early as their registers allow, and each slice issues
+    // its reads before its share of the fold: the group's scales after the first product, the next channel
+    // block's weight fragments (slice by slice, as the last token block releases them).  The last channel
+    // block follows the stage barrier, reads the next stage's activation fragments as its products release
+    // them, and spreads the direct loads of stage kt + 2 over its products.
+    auto bm_stage = [&](int kt, int buf, auto mode_c) __attribute__((always_inline)) {
+      constexpr int MODE = decltype(mode_c)::value;
+      const char* stage = smem + SCR + buf * STAGE;
+      const char* next = smem + SCR + (buf ^ 1) * STAGE;
+      // the previous group's last block is folded during this stage's first block, with that group's scales
+      const float p_sa = c_sa[TM - 1], p_sw = c_sw[TN - 1];
+      static_assert(NB % 2 == 0, "blocks alternate between the two partial sets, block 0 in set 0");
+      static_for<NB>([&](auto b_c) __attribute__((always_inline)) {
+        constexpr int b = decltype(b_c)::value, i = b / TM, j = b % TM, cur = b & 1;
+        constexpr int pb = (b + NB - 1) % NB, pi = pb / TM, pj = pb % TM;  // the block folded meanwhile
+        if constexpr (b == LAST && MODE != 2) {
+          // every wave's reads of this stage are done and stage kt + 1 has landed: the barrier publishes
+          // both, then the next stage's fragments are read and stage kt + 2 refills `buf`
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<0>();
+          __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+          barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        static_for<SLICES>([&](auto s_c) __attribute__((always_inline)) {
+          constexpr int s = decltype(s_c)::value;
+          if constexpr (s == 0) part[cur] = MF::run(fas[s], fbs[j][s], Acc{});
+          else part[cur] = MF::run(fas[s], fbs[j][s], part[cur]);
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (b == 0 && s == 0) read_scales(kt);
+          if constexpr (j == TM - 1) {  // slice s of the weight fragments is free
+            if constexpr (i + 1 < TN) fas[s] = MF::template load<BK>(stage, wrow_n + (i + 1) * 32, s, lane);
+            else if constexpr (MODE != 2) fas[s] = MF::template load<BK>(next, wrow_n, s, lane);
+          }
+          if constexpr (i == TN - 1 && MODE != 2) {
+            fbs[j][s] = MF::template load<BK>(next + A_BYTES, wrow_m + j * 32, s, lane);
+            if constexpr (MODE == 0) {
+              constexpr int slot = j * SLICES + s, SLOTS = TM * SLICES;
+#pragma unroll
+              for (int q = slot * LOADS / SLOTS; q < (slot + 1) * LOADS / SLOTS; q++) issue_load(kt + 2, buf, q);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          const float fsa = b == 0 ? p_sa : c_sa[pj];
+          const float fsw = b == 0 ? p_sw : c_sw[pi];
+          fold_chunk(facc[pi][pj], part[cur ^ 1], fsa, fsw, std::integral_constant<int, s * FOLD_PER>(),
+                     std::integral_constant<int, FOLD_PER>());
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      });
+    };
+    int kt = 0;
+    if constexpr (BMAJ) {
+      for (; kt + 2 < nk; kt++) bm_stage(kt, kt & 1, std::integral_constant<int, 0>());
+      if (kt + 1 < nk) {
+        bm_stage(kt, kt & 1, std::integral_constant<int, 1>());
+        kt++;
+      }
+      bm_stage(kt, kt & 1, std::integral_constant<int, 2>());
+    } else {
+      for (; kt + 2 < nk; kt++) stage_body(kt, kt & 1, std::integral_constant<int, 0>());
+      if (kt + 1 < nk) {
+        stage_body(kt, kt & 1, std::integral_constant<int, 1>());
+        kt++;
+      }
+      stage_body(kt, kt & 1, std::integral_constant<int, 2>());
+    }
     // every wave is done reading the stage buffers (and the scale ring) of this tile
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     barrier();
@@ -617,6 +763,10 @@ void block_gemm_kernel(const GemmArgs a) {
       tile_origin(t, m0, n0);
       plan_loads(m0, n0, tl);
       issue_stage(0, 0);
+    }
+    if constexpr (BMAJ) {  // the last group's last block, while the next tile's first stage lands
+      fold_chunk(facc[TN - 1][TM - 1], part[(TN * TM - 1) & 1], c_sa[TM - 1], c_sw[TN - 1],
+                 std::integral_constant<int, 0>(), std::integral_constant<int, 16>());
     }
 
     // Tile-local coordinates (32-bit): lane holds token ml = wrow_m + 32 j and channels
