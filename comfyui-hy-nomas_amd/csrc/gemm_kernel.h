@@ -199,6 +199,19 @@ __device__ __forceinline__ void g2lds4(const void* g, char* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_wave_base, 4, 0, 0);
 }
 
+// The same through a raw buffer descriptor: lane i's bytes at base + soffset + voffset_i (voffset in a
+// VGPR, soffset in an SGPR), so a stage's loads need no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  // no stride, every 32-bit offset in range, gfx9 raw-buffer format word
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ void b2lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_wave_base, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void b2lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_wave_base, 4, voff, soff, 0, 0);
+}
+
 // Wait until at most N of this wave's vector-memory loads are outstanding (they retire in issue order).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -325,6 +338,9 @@ void block_gemm_kernel(const GemmArgs a) {
   uint32_t woff[A_KB], aoff[B_KB];
   const float* scbase[SC_PER_WAVE > 0 ? SC_PER_WAVE : 1];
   uint32_t scoff[SC_PER_WAVE > 0 ? SC_PER_WAVE : 1];
+  // buffer descriptors of the tile's operand panels and scale rows (the direct loads add a per-lane byte
+  // offset and the stage's byte offset)
+  __amdgpu_buffer_rsrc_t wrsrc, arsrc, screc[SC_PER_WAVE > 0 ? SC_PER_WAVE : 1];
   auto plan_loads = [&](int64_t m0, int64_t n0, int lane) {
     wbase = a.qw + n0 * a.ldw;
     abase = a.qa + m0 * a.lda;
@@ -363,18 +379,23 @@ void block_gemm_kernel(const GemmArgs a) {
         scoff[u] = 0;
       }
     }
+    wrsrc = buffer_rsrc(wbase);
+    arsrc = buffer_rsrc(abase);
+#pragma unroll
+    for (int u = 0; u < SC_PER_WAVE; u++) screc[u] = buffer_rsrc(scbase[u]);
   };
   // load q (0 <= q < LOADS) of stage kt: weight rows, then activation rows, then scales
   auto issue_load = [&](int kt, int buf, int q) __attribute__((always_inline)) {
     char* base = smem + SCR + buf * STAGE;
     if (q < A_KB) {
-      g2lds16(wbase + (int64_t)kt * BK + woff[q], base + (wave + NW * q) * 1024);
+      b2lds16(wrsrc, woff[q], (uint32_t)kt * BK, base + (wave + NW * q) * 1024);
     } else if (q < A_KB + B_KB) {
       const int u = q - A_KB;
-      g2lds16(abase + (int64_t)kt * BK + aoff[u], base + A_BYTES + (wave + NW * u) * 1024);
+      b2lds16(arsrc, aoff[u], (uint32_t)kt * BK, base + A_BYTES + (wave + NW * u) * 1024);
     } else {
       const int u = q - A_KB - B_KB;
-      g2lds4(scbase[u] + kt / STAGES_PER_GROUP + scoff[u], smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
+      b2lds4(screc[u], scoff[u] * 4u, (uint32_t)(kt / STAGES_PER_GROUP) * 4u,
+             smem + (kt % (NS + 1)) * SC_BYTES + (wave + NW * u) * 256);
     }
   };
   auto issue_stage = [&](int kt, int buf) {
