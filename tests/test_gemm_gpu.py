@@ -99,6 +99,34 @@ def test_int8_gemm_bit_exact(dev, m, n, k, per_channel, with_bias):
     assert max_abs_rel(got.float().numpy(), fp64_dequant_product(qa, sa, w.numpy(), sw.numpy(), bias)) < 1e-2
 
 
+@pytest.mark.parametrize("m,n,k,epilogue", [
+    (64, 288, 256, None), (300, 1000, 384, None), (513, 520, 640, None), (40, 4096, 256, None),
+    (130, 384, 384, None), (40, 4096, 256, "gelu_quant"), (130, 384, 384, "gelu_quant")])
+def test_g128_stage_counts_and_ragged_tiles(dev, m, n, k, epilogue):
+    """The g128 layout's block-major loop: two, three and five 128-deep stages (the last two stages of a tile
+    take their own code paths, and a tile's first stage folds no previous block), tiles cut by M and N,
+    N not a multiple of 8 (scalar stores), and the GELU + requantization epilogue; bit-exact vs the oracle."""
+    from hy_nomas import kernels
+
+    print(f"g128 int8 m={m} n={n} k={k} epilogue={epilogue}", flush=True)
+    x = outlier_input(m, k, seed=m + 7 * n)
+    w, sw, bias = int8_weights(n, k, seed=n + 3 * k)
+    qa, sa = oracle.quantize(x, 128)
+    args = (torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev), bias.to(dev))
+    if epilogue is None:
+        out = kernels.block_gemm(*args)
+        ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+        got, want = out.cpu(), torch.from_numpy(ref).to(torch.bfloat16)
+        diff = (got != want).nonzero()
+        assert diff.numel() == 0, f"{len(diff)} outputs differ from the oracle, first {diff[:3].tolist()}"
+    else:
+        # the codes of the GEMM's own bf16 GELU output: the quantization runs on what the GELU epilogue writes
+        gelu = kernels.block_gemm(*args, epilogue="gelu")
+        qh, sh = kernels.block_gemm(*args, epilogue="gelu_quant")
+        q2, s2 = kernels.quantize_activations(gelu)
+        assert torch.equal(qh.cpu(), q2.cpu()) and torch.equal(sh.cpu(), s2.cpu())
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
 def test_int8_gemm_out_dtypes(dev, out_dtype):
     from hy_nomas import kernels
@@ -152,7 +180,8 @@ def test_gelu_epilogues(dev, per_channel):
     assert torch.equal(qh.cpu(), q2.cpu()) and torch.equal(sh.cpu(), s2.cpu())
 
 
-@pytest.mark.parametrize("m,n,k,group", [(300, 512, 1024, 128), (1024, 1536, 3072, 128), (200, 384, 2048, None)])
+@pytest.mark.parametrize("m,n,k,group", [(300, 512, 1024, 128), (1024, 1536, 3072, 128), (77, 384, 256, 128),
+                                         (130, 640, 384, 128), (200, 384, 2048, None)])
 def test_fp8_gemm(dev, m, n, k, group):
     from hy_nomas import kernels, pixelumm
 
