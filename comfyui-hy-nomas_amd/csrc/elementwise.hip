@@ -72,7 +72,10 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
   const int nchunk = (int)(D / 8);
   const int64_t b = blockIdx.x / blocks_per_batch;
   const int jb = blockIdx.x % blocks_per_batch;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // quantizing rows: the wave index is made uniform, so the row index and the code and scale output bases
+  // stay in scalar registers (the plain adaLN rows measured faster without it)
+  const int lane = threadIdx.x & 63;
+  const int wave = QUANT ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : (int)(threadIdx.x >> 6);
   const int64_t l = (int64_t)jb * kRowWaves + wave;
   const bool live = l < L;  // whole wave
   const int64_t r = b * L + (live ? l : L - 1);
@@ -192,6 +195,73 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
     }
     if (lane == 0) s[r] = gs;
     return;
+  }
+  if constexpr (QUANT && !PT && KEEP && FULL && DT == HN_DTYPE_BF16) {
+    // g128 codes of a finite row whose groups all take the fast quotient (the usual case): every chunk is
+    // modulated and rounded first, the group peaks reduced together, and one wave vote replaces the
+    // per-group branches; codes and scales are those of the general loop below.
+    if (__builtin_expect(finite, 1)) {
+      float pk[CPL];
+#pragma unroll
+      for (int i = 0; i < CPL; i++) {
+        const int c = lane + 64 * i;
+        const float4 g0 = fac[c], g1 = fac[nchunk + c], h0 = fac[2 * nchunk + c], h1 = fac[3 * nchunk + c];
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        float peak = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const uint32_t w = bf16x2_finite(__builtin_fmaf(f[i][j] * rstd, g[j], h[j]),
+                                           __builtin_fmaf(f[i][j + 1] * rstd, g[j + 1], h[j + 1]));
+          f[i][j] = __uint_as_float(w << 16);
+          f[i][j + 1] = __uint_as_float(w & 0xffff0000u);
+          peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j]));
+          peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j + 1]));
+        }
+        pk[i] = peak;
+      }
+      bool all_fast = true;
+#pragma unroll
+      for (int i = 0; i < CPL; i++) {
+        pk[i] = row16_max_nonneg(pk[i]);  // D % 128 == 0: a DPP row of 16 lanes holds one group
+        all_fast = all_fast && fast_group_i8(pk[i]);
+      }
+      if (__builtin_expect(__all(all_fast), 1)) {
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+          const float gs = int8_scale_fast(pk[i]);
+          const FastDivI8 div(gs);
+          int cd[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float v = div(f[i][j]);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+          }
+          st_nt8(qrow + 512 * i, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
+          srow[4 * i] = gs;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPL; i++) {
+          const float gs = fast_group_i8(pk[i]) ? int8_scale_fast(pk[i]) : int8_scale(pk[i]);
+          int cd[8];
+          if (fast_group_i8(pk[i])) {
+            const FastDivI8 div(gs);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+              const float v = div(f[i][j]);
+              cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) cd[j] = round_i8<ROUND>(f[i][j] / gs);
+          }
+          st_nt8(qrow + 512 * i, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
+          srow[4 * i] = gs;
+        }
+      }
+      return;
+    }
   }
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
