@@ -475,6 +475,49 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
 
 // ---------------------------------------------------------------------------------------------
 // QK RMSNorm + interleaved RoPE                                  (fused.py:65-91)
+
+// Sum over aligned groups of W lanes (W = 8, 16 or 32), every lane of a group getting the total, in the
+// butterfly order of xor shuffles with masks 1, 2, 4, ...  Inside a DPP row the steps are quad_perm and
+// mirror moves: after the two quad steps every lane of a quad holds the same value, so the half-row
+// mirror delivers the xor-4 partner's value and the row mirror the xor-8 partner's.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(W == 8 || W == 16 || W == 32, "group of 8, 16 or 32 lanes");
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  if constexpr (W >= 16) v += dpp_f<0x140>(v);
+  if constexpr (W == 32) v += shfl_xor_f(v, 16, 32);
+  return v;
+}
+
+// One lane's 8 dims of a normalized (and rotated) head row: bf16(bf16(x * r) * w), then the interleaved
+// rotation.  HW: the roundings use the hardware conversion, equal to rbf16 on every non-NaN input.
+template <bool ROPE, bool HW>
+__device__ __forceinline__ void qk_rows8(const float* f, float r, const float* wv, const float* cv, const float* sv,
+                                         float* o) {
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    float ne, no;
+    if constexpr (HW) {
+      const uint32_t a = bf16x2_finite(f[i] * r, f[i + 1] * r);
+      const uint32_t b = bf16x2_finite(__uint_as_float(a << 16) * wv[i], __uint_as_float(a & 0xffff0000u) * wv[i + 1]);
+      ne = __uint_as_float(b << 16);
+      no = __uint_as_float(b & 0xffff0000u);
+    } else {
+      ne = rbf16(rbf16(f[i] * r) * wv[i]);
+      no = rbf16(rbf16(f[i + 1] * r) * wv[i + 1]);
+    }
+    if constexpr (ROPE) {
+      o[i] = ne * cv[i] - no * sv[i];
+      o[i + 1] = no * cv[i + 1] + ne * sv[i + 1];
+    } else {
+      o[i] = ne;
+      o[i + 1] = no;
+    }
+  }
+}
+
 // W = D / 8 lanes per head, lane j holding dims [8j, 8j + 8).  Each W-lane group normalizes G heads of
 // one token (G = 6, 4, 2 or 1, the largest that divides the head count): the weight and the token's
 // rotary rows are loaded once per group, and the group's G head rows are all in flight before the
@@ -517,26 +560,25 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(const uint16_t* __res
       se = __builtin_fmaf(f[i], f[i], se);
       so = __builtin_fmaf(f[i + 1], f[i + 1], so);
     }
-#pragma unroll
-    for (int m = 1; m < W; m <<= 1) {
-      se += shfl_xor_f(se, m, W);
-      so += shfl_xor_f(so, m, W);
-    }
+    se = group_sum<W>(se);
+    so = group_sum<W>(so);
     const float r = 1.0f / __builtin_sqrtf((se + so) / (float)D + eps);
+    // A NaN reaching any rounding propagates into the outputs it feeds, so outputs free of NaN mean the
+    // hardware roundings saw no NaN and equal the software ones; a lane with a NaN output recomputes its
+    // dims with the software rounding and torch's NaN code.
     float o[8];
+    qk_rows8<ROPE, true>(f, r, wv, cv, sv, o);
+    bool nan = false;
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const float ne = rbf16(rbf16(f[i] * r) * wv[i]);
-      const float no = rbf16(rbf16(f[i + 1] * r) * wv[i + 1]);
-      if constexpr (ROPE) {
-        o[i] = ne * cv[i] - no * sv[i];
-        o[i + 1] = no * cv[i + 1] + ne * sv[i + 1];
-      } else {
-        o[i] = ne;
-        o[i + 1] = no;
-      }
+    for (int i = 0; i < 8; i += 2) nan |= __builtin_isunordered(o[i], o[i + 1]);
+    uint4 packed;
+    if (__builtin_expect(nan, 0)) {
+      qk_rows8<ROPE, false>(f, r, wv, cv, sv, o);
+      packed = narrow8x<HN_DTYPE_BF16, false>(o);
+    } else {
+      packed = narrow8x<HN_DTYPE_BF16, true>(o);
     }
-    if (live) st_nt16(y + (bl * H + h0 + g) * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+    if (live) st_nt16(y + (bl * H + h0 + g) * D + j * 8, packed);
   }
 }
 
@@ -580,9 +622,7 @@ __global__ __launch_bounds__(256) void pixelumm_qk_kernel(const uint16_t* __rest
 #pragma unroll
     for (int i = 0; i < 8; i++) sq = __builtin_fmaf(f[i], f[i], sq);
     // lanes 0-7 reduce the T half, lanes 8-15 the HW half
-    sq += shfl_xor_f(sq, 1, 16);
-    sq += shfl_xor_f(sq, 2, 16);
-    sq += shfl_xor_f(sq, 4, 16);
+    sq = group_sum<8>(sq);
     const float rr = 1.0f / __builtin_sqrtf(sq / (float)(D / 2) + eps);
     float v[8];
 #pragma unroll
@@ -593,7 +633,13 @@ __global__ __launch_bounds__(256) void pixelumm_qk_kernel(const uint16_t* __rest
       const float p = __shfl(v[i], (threadIdx.x & 63) ^ partner_xor, 64);
       o[i] = first ? v[i] * cv[i] - p * sv[i] : v[i] * cv[i] + p * sv[i];
     }
-    if (live) st_nt16(y + (t * H + h0 + g) * D + j * 8, narrow8<HN_DTYPE_BF16>(o));
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) nan |= __builtin_isunordered(o[i], o[i + 1]);
+    uint4 packed;
+    if (__builtin_expect(nan, 0)) packed = narrow8x<HN_DTYPE_BF16, false>(o);
+    else packed = narrow8x<HN_DTYPE_BF16, true>(o);
+    if (live) st_nt16(y + (t * H + h0 + g) * D + j * 8, packed);
   }
 }
 

@@ -209,6 +209,81 @@ def test_qk_norm_rope_head_groups(dev, h, d):
         assert (got.cpu() != ora).float().mean().item() < 1e-2
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_qk_norm_rope_nonfinite(dev, d):
+    """NaN and inf inputs.  A head holding a NaN comes out as torch's NaN code 0x7FC0 in every dim; a head
+    holding an inf has r = 0, so its inf dim (and, with the rotation, that dim's pair partner) is NaN and the
+    rest zero; a head whose sum of squares overflows comes out as zeros; a NaN weight gives 0x7FC0 in its
+    dim (and its pair partner) of every head.  Every other output equals the same call on clean data bit
+    for bit."""
+    from hy_nomas import fused
+
+    print(f"qk_norm_rope nonfinite d={d}", flush=True)
+    b, l, h = 1, 9, 6
+    g = seeded(300 + d)
+    x = bf(torch.randn(b, l, h, d, generator=g) * 3)
+    w = bf(torch.rand(d, generator=g) + 0.5)
+    ang = torch.rand(l, d, generator=g) * 6.28
+    rope = (ang.cos().to(dev), ang.sin().to(dev))
+    clean = x.clone()
+    x[0, 1, 2, 5] = float("nan")
+    x[0, 3, 0, d - 1] = float("inf")
+    x[0, 4, 5, 7] = -float("inf")
+    x[0, 6, 3] = 3e38   # the sum of squares overflows: r = 0
+    nan_code = 0x7FC0
+
+    def pair(i, rotated):
+        return [i & ~1, i | 1] if rotated else [i]
+
+    for rp in (None, rope):
+        got = fused.qk_norm_rope(x.to(dev), w.to(dev), rp).cpu()
+        ref = fused.qk_norm_rope(clean.to(dev), w.to(dev), rp).cpu()
+        bits = got.view(torch.int16)
+        assert (bits[0, 1, 2] == nan_code).all()
+        for t, k, i in ((3, 0, d - 1), (4, 5, 7)):
+            nan_dims = pair(i, rp is not None)
+            assert (bits[0, t, k, nan_dims] == nan_code).all()
+            zero_dims = [c for c in range(d) if c not in nan_dims]
+            assert (got[0, t, k, zero_dims].float() == 0).all()
+        assert (got[0, 6, 3].float() == 0).all()
+        touched = torch.zeros(l, h, dtype=torch.bool)
+        for t, k in ((1, 2), (3, 0), (4, 5), (6, 3)):
+            touched[t, k] = True
+        assert torch.equal(got[0][~touched], ref[0][~touched])
+        ora = torch.from_numpy(oracle.qk_norm_rope(x, w, None if rp is None else (rp[0].cpu(), rp[1].cpu())))
+        assert torch.equal(ora.isnan(), got.float().isnan())
+        # a NaN weight in dim 5: that dim (and dim 4, its rotation partner) of every head is NaN
+        wn = w.clone()
+        wn[5] = float("nan")
+        got = fused.qk_norm_rope(clean.to(dev), wn.to(dev), rp).cpu()
+        bad = pair(5, rp is not None)
+        keep = [i for i in range(d) if i not in bad]
+        assert (got.view(torch.int16)[..., bad] == nan_code).all()
+        assert torch.equal(got[..., keep], ref[..., keep])
+
+
+def test_pixelumm_qk_nonfinite(dev):
+    """A NaN in the T half of a head makes that half torch's NaN code 0x7FC0 (its norm is NaN); the head's HW
+    half and every other head equal the same call on clean data bit for bit."""
+    from hy_nomas import fused
+
+    n, h, d = 11, 6, 128
+    g = seeded(400)
+    x = bf(torch.randn(1, n, h, d, generator=g) * 3)
+    wt = bf(torch.rand(d // 2, generator=g) + 0.5).to(dev)
+    whw = bf(torch.rand(d // 2, generator=g) + 0.5).to(dev)
+    ang = torch.rand(n, d, generator=g) * 6.28
+    cos, sin = ang.cos().to(dev), ang.sin().to(dev)
+    ref = fused.pixelumm_qk(x.to(dev), wt, whw, cos, sin).cpu()
+    x[0, 4, 2, 17] = float("nan")
+    got = fused.pixelumm_qk(x.to(dev), wt, whw, cos, sin).cpu()
+    assert (got.view(torch.int16)[0, 4, 2, :64] == 0x7FC0).all()
+    assert torch.equal(got[0, 4, 2, 64:], ref[0, 4, 2, 64:])
+    keep = torch.ones(n, h, dtype=torch.bool)
+    keep[4, 2] = False
+    assert torch.equal(got[0][keep], ref[0][keep])
+
+
 @pytest.mark.parametrize("h", [1, 2, 3, 6, 24])
 def test_pixelumm_qk_head_groups(dev, h):
     """The PixelUMM kernel's head groups: each head of a multi-head call equals a one-head call bit for bit."""
