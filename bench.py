@@ -35,7 +35,7 @@ M = 32768
 HIDDEN = 3072
 # Memory-side bytes per headline step (4 GEMM launches) from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this
 # script, scaled by a plain-copy calibration (FETCH x2.0, WRITE x1.0); profiles/block_gemm_int8_per_token_M32768.md
-TRAFFIC_BYTES_PER_STEP = 7.26e9
+TRAFFIC_BYTES_PER_STEP = 6.56e9
 SLEEP_CYCLES = 2e8           # ~80 ms of spin before each timed region
 HOT_S = 0.1                  # seconds of untimed passes between the spin and the timed region
 HOT_MAX_LAUNCHES = 2000

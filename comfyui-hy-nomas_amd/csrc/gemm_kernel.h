@@ -384,14 +384,25 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < SC_PER_WAVE; u++) screc[u] = buffer_rsrc(scbase[u]);
   };
+  const int nk = (int)(a.K / BK);
+  // int8 per-token tiles (whole-K int32 sums: the order of the stages does not change them) walk K backwards
+  // on every other tile of the workgroup.  The tiles an XCD runs next share the activation panels of the
+  // ones it just finished, and then start on the stages those read last, which are still in L2.  (fp8 sums
+  // are fp32 and keep one order.)
+  constexpr bool SERP = !G128 && KIND == HN_KIND_INT8;
+  bool krev = false;
+  // byte offset of stage kt within the K extent
+  auto kofs = [&](int kt) __attribute__((always_inline)) {
+    return (uint32_t)(SERP && krev ? nk - 1 - kt : kt) * BK;
+  };
   // load q (0 <= q < LOADS) of stage kt: weight rows, then activation rows, then scales
   auto issue_load = [&](int kt, int buf, int q) __attribute__((always_inline)) {
     char* base = smem + SCR + buf * STAGE;
     if (q < A_KB) {
-      b2lds16(wrsrc, woff[q], (uint32_t)kt * BK, base + (wave + NW * q) * 1024);
+      b2lds16(wrsrc, woff[q], kofs(kt), base + (wave + NW * q) * 1024);
     } else if (q < A_KB + B_KB) {
       const int u = q - A_KB;
-      b2lds16(arsrc, aoff[u], (uint32_t)kt * BK, base + A_BYTES + (wave + NW * u) * 1024);
+      b2lds16(arsrc, aoff[u], kofs(kt), base + A_BYTES + (wave + NW * u) * 1024);
     } else {
       const int u = q - A_KB - B_KB;
       b2lds4(screc[u], scoff[u] * 4u, (uint32_t)(kt / STAGES_PER_GROUP) * 4u,
@@ -404,7 +415,6 @@ void block_gemm_kernel(const GemmArgs a) {
   };
 
 
-  const int nk = (int)(a.K / BK);
   const int wrow_n = wn * TN * 32 + (lane & 31);  // this lane's A-fragment row within the weight tile
   const int wrow_m = wm * TM * 32 + (lane & 31);  // and B-fragment row within the activation tile
 
@@ -783,6 +793,7 @@ void block_gemm_kernel(const GemmArgs a) {
     if (more) {
       tile_origin(t, m0, n0);
       plan_loads(m0, n0, tl);
+      krev = !krev;
       issue_stage(0, 0);
     }
     if constexpr (BMAJ) {  // the last group's last block, while the next tile's first stage lands
