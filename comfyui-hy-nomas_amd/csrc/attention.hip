@@ -64,12 +64,6 @@ struct AttnArgs {
   int qblocks;
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr_a;
-
-__device__ __forceinline__ void g2lds16_a(const void* g, char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_a)lds_wave_base, 16, 0, 0);
-}
-
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }
 
 // max of x over lanes l and l ^ 32 (one v_permlane32_swap instead of an LDS permute)
@@ -100,8 +94,8 @@ void attention_kernel(const AttnArgs a) {
   for (int ks = 0; ks < 8; ks++) qf[ks] = *reinterpret_cast<const bf16x8*>(qbase + qi * a.sqi + 16 * ks + 8 * h2);
 
   // direct loads of one tile: wave w fills the 1 KB blocks w, w + 4, w + 8, w + 12 of the K tile (4 rows of
-  // 256 bytes each) and of the V^T tile (8 rows of 128 bytes), each lane 16 bytes at a 32-bit offset from a
-  // wave-uniform base
+  // 256 bytes each) and of the V^T tile (8 rows of 128 bytes), each lane 16 bytes at a fixed 32-bit offset
+  // from the tile's buffer descriptor (wave-uniform base: no per-lane 64-bit address arithmetic)
   uint32_t koff[4], voff[4];
 #pragma unroll
   for (int u = 0; u < 4; u++) {
@@ -113,11 +107,11 @@ void attention_kernel(const AttnArgs a) {
   auto issue_tile = [&](int64_t j0, int buf) {
     char* kt = smem + buf * kAttnStage;
     char* vt = kt + kKTile;
-    const char* kb = kbase + j0 * kstride;
-    const char* vb = vbase + j0 * 2;
+    const __amdgpu_buffer_rsrc_t kr = buffer_rsrc(kbase + j0 * kstride);
+    const __amdgpu_buffer_rsrc_t vr = buffer_rsrc(vbase + j0 * 2);
     if (j0 + kBK <= a.Lk) {
 #pragma unroll
-      for (int u = 0; u < 4; u++) g2lds16_a(kb + koff[u], kt + (wave + 4 * u) * 1024);
+      for (int u = 0; u < 4; u++) b2lds16(kr, koff[u], 0, kt + (wave + 4 * u) * 1024);
     } else {
       // the last tile: rows past the last key re-read it (their scores are masked)
       const int last = (int)(a.Lk - 1 - j0);
@@ -125,11 +119,11 @@ void attention_kernel(const AttnArgs a) {
       for (int u = 0; u < 4; u++) {
         const int krow = (wave + 4 * u) * 4 + lane / 16, kphys = lane % 16;
         const int r = krow < last ? krow : last;
-        g2lds16_a(kb + ((uint32_t)r * kstride + (uint32_t)((kphys ^ (krow & 15)) << 4)), kt + (wave + 4 * u) * 1024);
+        b2lds16(kr, (uint32_t)r * kstride + (uint32_t)((kphys ^ (krow & 15)) << 4), 0, kt + (wave + 4 * u) * 1024);
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) g2lds16_a(vb + voff[u], vt + (wave + 4 * u) * 1024);
+    for (int u = 0; u < 4; u++) b2lds16(vr, voff[u], 0, vt + (wave + 4 * u) * 1024);
   };
 
   v16f_a oacc[4];
@@ -142,15 +136,16 @@ void attention_kernel(const AttnArgs a) {
   const int kswz = l32 & 15, vswz = (l32 >> 1) & 7;   // the lane's rows' swizzles (rows 32 i + l32)
 
   const int64_t nt = (a.Lk + kBK - 1) / kBK;
-  issue_tile(0, 0);
-  for (int64_t t = 0; t < nt; t++) {
-    const int buf = (int)(t & 1);
+  // tile t in stage buffer BUF (a constant, so the buffer offset rides in the LDS reads' immediate field
+  // and the lane's fragment offsets stay fixed across the loop)
+  auto tile = [&](int64_t t, auto buf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
     // tile t has landed for every wave, and every wave is done with the buffer tile t + 1 refills
     wait_vm0();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    if (t + 1 < nt) issue_tile((t + 1) * kBK, buf ^ 1);
-    const char* kt = smem + buf * kAttnStage;
+    if (t + 1 < nt) issue_tile((t + 1) * kBK, BUF ^ 1);
+    const char* kt = smem + BUF * kAttnStage;
     const char* vt = kt + kKTile;
     const int64_t j0 = t * kBK;
 
@@ -165,13 +160,14 @@ void attention_kernel(const AttnArgs a) {
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], ks == 0 ? v16f_a{} : s[kb], 0, 0, 0);
       }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
+      // register r of block kb holds key j0 + 32 kb + 8 (r / 4) + (r % 4) + 4 h2: a constant per register
+      // against one per-lane limit
+      const int lim = (int)(a.Lk - j0) - 4 * h2;
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int key = (int)(j0 - a.Lk) + 32 * kb + 8 * (r / 4) + 4 * h2 + (r % 4);
-          if (key >= 0) s[kb][r] = -__builtin_inff();
-        }
+        for (int r = 0; r < 16; r++)
+          if (32 * kb + 8 * (r / 4) + (r % 4) >= lim) s[kb][r] = -__builtin_inff();
     }
     // online softmax: the tile's max for this query (both lanes), then the lazy move of the reference max
     float mx = s[0][0];
@@ -218,6 +214,11 @@ void attention_kernel(const AttnArgs a) {
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, bi), oacc[db], 0, 0, 0);
         }
       }
+  };
+  issue_tile(0, 0);
+  for (int64_t t = 0; t < nt; t += 2) {
+    tile(t, std::integral_constant<int, 0>());
+    if (t + 1 < nt) tile(t + 1, std::integral_constant<int, 1>());
   }
   // normalize and store: lane holds query l32, dims 32 db + 8 rr + 4 h2 + 0..3 in registers 4 rr .. 4 rr + 3
   const float ltot = lsum + __shfl_xor(lsum, 32);

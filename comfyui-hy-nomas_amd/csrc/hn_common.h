@@ -216,6 +216,32 @@ __device__ __forceinline__ uint32_t bf16x2_finite(float a, float b) {
 }
 
 // ----------------------------------------------------------------------------------------------
+// direct-to-LDS loads (gfx950)
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Wave-wide direct-to-LDS loads: lane i's 16 (or 4) bytes from g land at lds_wave_base + i * 16 (or 4).
+__device__ __forceinline__ void g2lds16(const void* g, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void g2lds4(const void* g, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_wave_base, 4, 0, 0);
+}
+
+// The same through a raw buffer descriptor: lane i's bytes at base + soffset + voffset_i (voffset in a
+// VGPR, soffset in an SGPR), so a stage's loads need no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base) {
+  // no stride, every 32-bit offset in range, gfx9 raw-buffer format word
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+__device__ __forceinline__ void b2lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_wave_base, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void b2lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)lds_wave_base, 4, voff, soff, 0, 0);
+}
+
+// ----------------------------------------------------------------------------------------------
 // cross-lane reductions (wave64)
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask, int width = 64) { return __shfl_xor(v, mask, width); }
