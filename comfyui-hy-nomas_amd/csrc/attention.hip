@@ -132,6 +132,13 @@ void attention_kernel(const AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; r++) oacc[db][r] = 0.0f;
   float m = -__builtin_inff();  // reference max of the scaled scores (base-2 units), shared by lanes l, l ^ 32
+  // -m / (scale log2(e)) in every register: the score products start from it, so the scores come out already
+  // relative to the reference and a probability is exp2(s scale log2(e)).  0 until the first tile sets m.
+  v16f_a mref;
+#pragma unroll
+  for (int r = 0; r < 16; r++) mref[r] = 0.0f;
+  const float inv_scale = 1.0f / a.scale_log2;
+  float mref_m = 0.0f;  // the reference mref holds (m', base-2 units)
   float lsum = 0.0f;            // this lane's partial sum of the probabilities
   const int kswz = l32 & 15, vswz = (l32 >> 1) & 7;   // the lane's rows' swizzles (rows 32 i + l32)
 
@@ -157,7 +164,7 @@ void attention_kernel(const AttnArgs a) {
       for (int kb = 0; kb < 2; kb++) {
         const bf16x8 af =
             *reinterpret_cast<const bf16x8*>(kt + (32 * kb + l32) * 256 + (((2 * ks + h2) ^ kswz) << 4));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], ks == 0 ? v16f_a{} : s[kb], 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], ks == 0 ? mref : s[kb], 0, 0, 0);
       }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
       // register r of block kb holds key j0 + 32 kb + 8 (r / 4) + (r % 4) + 4 h2: a constant per register
@@ -169,15 +176,19 @@ void attention_kernel(const AttnArgs a) {
         for (int r = 0; r < 16; r++)
           if (32 * kb + 8 * (r / 4) + (r % 4) >= lim) s[kb][r] = -__builtin_inff();
     }
-    // online softmax: the tile's max for this query (both lanes), then the lazy move of the reference max
+    // online softmax: the tile's max for this query (both lanes), then the lazy move of the reference max.
+    // The scores hold s - m' / (scale log2(e)), m' the reference their products started from (m after the
+    // first tile), so the tile's max in base-2 units is mx scale log2(e) + m'.
     float mx = s[0][0];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int r = 0; r < 16; r++) mx = __builtin_fmaxf(mx, s[kb][r]);
-    const float mt = max_xor32(mx) * a.scale_log2;
-    const bool grow = mt > m + kSlack;  // always true for the first tile (m = -inf)
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    const float mrel = max_xor32(mx) * a.scale_log2;  // the tile's max relative to m'
+    // m' = m outside the move below; the first tile (m = -inf) always moves it
+    if (__builtin_amdgcn_ballot_w64(!(mrel + mref_m <= m + kSlack)) != 0) {
+      const float mt = mrel + mref_m;
+      const bool grow = mt > m + kSlack;
       const float mnew = grow ? mt : m;
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 where m stays, 0 for the first tile
       m = mnew;
@@ -186,16 +197,25 @@ void attention_kernel(const AttnArgs a) {
       for (int db = 0; db < 4; db++)
 #pragma unroll
         for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
+      // this tile's scores moved to the new reference, and the next tiles' products start from it
+      const float delta = (mref_m - m) * inv_scale;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s[kb][r] += delta;
+      mref_m = m;
+      const float mr = -m * inv_scale;
+#pragma unroll
+      for (int r = 0; r < 16; r++) mref[r] = mr;
     }
-    // probabilities (base-2 exponent of the scaled score minus the reference), this lane's sum, bf16 pairs
-    const float nm = -m;
+    // probabilities exp2(s scale log2(e)) against the reference, this lane's sum, bf16 pairs
     uint32_t pk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int p = 0; p < 8; p++) {
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p], a.scale_log2, nm));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][2 * p + 1], a.scale_log2, nm));
+        const float e0 = __builtin_amdgcn_exp2f(s[kb][2 * p] * a.scale_log2);
+        const float e1 = __builtin_amdgcn_exp2f(s[kb][2 * p + 1] * a.scale_log2);
         lsum += e0 + e1;
         pk[kb][p] = bf16x2_finite(e0, e1);
       }
