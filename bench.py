@@ -349,18 +349,22 @@ def dit_block(dev, gen, steps, warmup, per_token):
     out = {"activations": "per-token x per-channel" if per_token else "g128 (reference layout)"}
     ops = 2 * (lv + lt) * sum(n * k for _, k, n in STACK)
     # the block's attention call on the same operands: head-major q, k, v [B, H, L, D] as the QKV epilogue
-    # writes them, image and text tokens together
+    # writes them, image and text tokens together (SDPA); for the HIP kernel, q and k head-major and v in the
+    # V^T layout the QKV epilogue writes for it
     hm = torch.randn(3, 1, heads, lv + lt, d // heads, generator=gen, device=dev).to(torch.bfloat16)
+    vt = attention.transpose_values(hm[2])
     att_flops = 4 * (lv + lt) ** 2 * d
+    att_calls = {"sdpa": lambda: attention.attention_heads(hm[0], hm[1], hm[2], "sdpa"),
+                 "hip": lambda: attention.attention_hip(hm[0].transpose(1, 2), hm[1].transpose(1, 2), vt, lv + lt)}
     with torch.no_grad():
         for backend in ("sdpa", "hip"):
             ms, _ = time_launches([lambda: blk.forward(img, txt, mods[0], mods[1], rope, backend)], steps, warmup)
-            att_ms, _ = time_launches([lambda: attention.attention_heads(hm[0], hm[1], hm[2], backend)], steps, warmup)
+            att_ms, _ = time_launches([att_calls[backend]], steps, warmup)
             lin_ms = ms - att_ms
             out[backend] = {"block_ms": round(ms, 3), "attention_ms": round(att_ms, 3),
                             "attention_TFLOPS": round(att_flops / (att_ms * 1e-3) / 1e12, 1),
                             "linear_path_ms": round(lin_ms, 3), "linear_TOPS": round(ops / (lin_ms * 1e-3) / 1e12, 1)}
-    del blk, img, txt, hm
+    del blk, img, txt, hm, vt
     torch.cuda.empty_cache()
     out["linear_ops"] = ops
     out["attention_flops"] = att_flops
@@ -368,19 +372,25 @@ def dit_block(dev, gen, steps, warmup, per_token):
 
 
 def attention_only(dev, gen, steps, warmup):
-    """The block's joint attention alone at 57344 + 256 tokens x 24 heads x 128 (head-major bf16 q, k, v as the
-    QKV epilogue writes them), on both backends: ms and TFLOPS (4 L^2 D H flops)."""
+    """The block's joint attention alone at 57344 + 256 tokens x 24 heads x 128, on the operands the block's QKV
+    epilogue writes for each backend: head-major bf16 q, k, v for SDPA; q and k head-major and v as V^T for the
+    HIP kernel.  ms and TFLOPS (4 L^2 D H flops); "hip_with_vt_copy" adds the V^T copy a caller with head-major
+    v makes (`attention.attention_heads`)."""
     from hy_nomas import attention
 
     length, heads = 57344 + 256, 24
     hm = torch.randn(3, 1, heads, length, 128, generator=gen, device=dev).to(torch.bfloat16)
+    vt = attention.transpose_values(hm[2])
     flops = 4 * length ** 2 * 128 * heads
     out = {"tokens": length, "heads": heads, "flops": flops}
+    calls = {"sdpa": lambda: attention.attention_heads(hm[0], hm[1], hm[2], "sdpa"),
+             "hip": lambda: attention.attention_hip(hm[0].transpose(1, 2), hm[1].transpose(1, 2), vt, length),
+             "hip_with_vt_copy": lambda: attention.attention_heads(hm[0], hm[1], hm[2], "hip")}
     with torch.no_grad():
-        for backend in ("sdpa", "hip"):
-            ms, _ = time_launches([lambda: attention.attention_heads(hm[0], hm[1], hm[2], backend)], steps, warmup)
-            out[backend] = {"ms": round(ms, 3), "TFLOPS": round(flops / (ms * 1e-3) / 1e12, 1)}
-    del hm
+        for name, fn in calls.items():
+            ms, _ = time_launches([fn], steps, warmup)
+            out[name] = {"ms": round(ms, 3), "TFLOPS": round(flops / (ms * 1e-3) / 1e12, 1)}
+    del hm, vt
     torch.cuda.empty_cache()
     return out
 

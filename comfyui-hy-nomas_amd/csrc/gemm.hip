@@ -186,11 +186,12 @@ extern "C" int hn_block_gemm(const void* qa, int64_t lda, const float* sa, int64
   return launch_kind<HN_KIND_FP8>(a, g128, epilogue, out_dtype, st);
 }
 
-extern "C" int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
-                            const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
-                            int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
-                            const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
-                            int64_t L_total, int64_t l_offset, void* stream) {
+static int qkv_heads_impl(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                          const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
+                          int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
+                          const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
+                          int64_t L_total, int64_t l_offset, void* vt, int64_t svb, int64_t svh, int64_t svd,
+                          void* stream) {
   using namespace hn;
   HN_REQUIRE(B >= 0 && L >= 0 && hidden > 0 && K > 0, "hn_qkv_heads: bad shape");
   HN_REQUIRE(hidden % 128 == 0, "hn_qkv_heads: hidden=%lld is not a multiple of the head dim 128", (long long)hidden);
@@ -225,8 +226,36 @@ extern "C" int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_
   a.stage_store = 1;
   a.hm_L = L; a.hm_Ltot = L_total; a.hm_loff = l_offset; a.hm_hidden = hidden; a.hm_B = B;
   a.hm_wq = q_norm_w; a.hm_wk = k_norm_w; a.hm_cos = cos_t; a.hm_sin = sin_t; a.hm_eps = eps;
+  a.hm_vt = (uint16_t*)vt; a.hm_svb = svb; a.hm_svh = svh; a.hm_svd = svd;
   hipStream_t st = (hipStream_t)stream;
   const bool g128 = group == 128 && (K != 128 || sw_rows == 128);
   if (kind == HN_KIND_INT8) return launch_group<HN_KIND_INT8, kEpiQkvHeads, HN_DTYPE_BF16>(a, g128, st);
   return launch_group<HN_KIND_FP8, kEpiQkvHeads, HN_DTYPE_BF16>(a, g128, st);
+}
+
+extern "C" int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                            const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
+                            int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
+                            const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
+                            int64_t L_total, int64_t l_offset, void* stream) {
+  return qkv_heads_impl(qa, lda, sa, ldsa, qw, ldw, sw, ldsw, sw_rows, bias, bias_dtype, B, L, hidden, K, group, kind,
+                        q_norm_w, k_norm_w, cos_t, sin_t, eps, out, L_total, l_offset, nullptr, 0, 0, 0, stream);
+}
+
+extern "C" int hn_qkv_heads_vt(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                               const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype,
+                               int64_t B, int64_t L, int64_t hidden, int64_t K, int64_t group, int kind,
+                               const float* q_norm_w, const float* k_norm_w, const float* cos_t, const float* sin_t,
+                               float eps, void* out, int64_t L_total, int64_t l_offset, void* vt, int64_t svb,
+                               int64_t svh, int64_t svd, void* stream) {
+  HN_REQUIRE(vt != nullptr && ((uintptr_t)vt & 15) == 0, "hn_qkv_heads_vt: V^T must be a 16-byte aligned pointer");
+  HN_REQUIRE(L % 32 == 0 && l_offset % 16 == 0,
+             "hn_qkv_heads_vt: L=%lld must be a multiple of 32 and l_offset=%lld of 16", (long long)L,
+             (long long)l_offset);
+  HN_REQUIRE(svd % 8 == 0 && svh % 8 == 0 && svb % 8 == 0 && svd >= l_offset + L && svh >= 128 * svd &&
+                 svb >= (hidden / 128) * svh,
+             "hn_qkv_heads_vt: V^T strides (%lld, %lld, %lld) must be multiples of 8 holding [B, H, 128, >= %lld]",
+             (long long)svb, (long long)svh, (long long)svd, (long long)(l_offset + L));
+  return qkv_heads_impl(qa, lda, sa, ldsa, qw, ldw, sw, ldsw, sw_rows, bias, bias_dtype, B, L, hidden, K, group, kind,
+                        q_norm_w, k_norm_w, cos_t, sin_t, eps, out, L_total, l_offset, vt, svb, svh, svd, stream);
 }

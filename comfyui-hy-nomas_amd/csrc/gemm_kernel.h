@@ -67,6 +67,11 @@ struct GemmArgs {
   const float* hm_cos;
   const float* hm_sin;
   float hm_eps;
+  // hm_vt: the v heads go to V^T instead (the attention kernel's layout): element (b, h, d, key p) at
+  // hm_vt + b hm_svb + h hm_svh + d hm_svd + p, keys of each 16-key group in the order 0-3, 8-11, 4-7, 12-15,
+  // token l at key hm_loff + l (hm_L % 32 == 0, hm_loff % 16 == 0)
+  uint16_t* hm_vt;
+  int64_t hm_svb, hm_svh, hm_svd;
 };
 
 // Internal epilogue id of the head-major QKV projection (entry point hn_qkv_heads).
@@ -1023,10 +1028,53 @@ void block_gemm_kernel(const GemmArgs a) {
             if (tl < 32 && wn * 128 < nrem) a.qs[(em0 + ml) * a.ldqs + (en0 + wn * 128) / 128] = gs;
           }
         } else if (STAGED && (EPI == kEpiQkvHeads || a.stage_store)) {
+          char* wst = smem + STG_OFF + wave * 32 * OPITCH;
+          bool to_vt = false;
+          if constexpr (EPI == kEpiQkvHeads) to_vt = a.hm_vt != nullptr && en0 + wn * 128 >= 2 * a.hm_hidden;
+          if (to_vt) {
+            // A v head to V^T: the wave's 128 dims x 32 tokens staged dim-major (row d of 64 bytes holds the
+            // 32 tokens in the 16-key-group order: bits 2 and 3 of the token index swapped), then each row's 64
+            // bytes written to its V^T row.  Lanes t and t ^ 1 (tokens 2p, 2p + 1) swap two of their four dims
+            // with a DPP move, so each writes one dim of both tokens as a packed pair: the even lane dims
+            // d0, d0 + 1, the odd lane d0 + 2, d0 + 3.
+            const int tk = tl & 31;
+            const bool odd = (tk & 1) != 0;
+            const int te = tk & ~1;
+            const int pcol = ((te & ~12) | ((te & 4) << 1) | ((te & 8) >> 1)) * 2;
+#pragma unroll
+            for (int i = 0; i < TN; i++)
+#pragma unroll
+              for (int rr = 0; rr < 4; rr++) {
+                const int d0 = i * 32 + rr * 8 + (tl >> 5) * 4;
+                const float v0 = MF::get(acc[i][j], rr * 4 + 0), v1 = MF::get(acc[i][j], rr * 4 + 1);
+                const float v2 = MF::get(acc[i][j], rr * 4 + 2), v3 = MF::get(acc[i][j], rr * 4 + 3);
+                const float r0 = dpp_f<0xB1>(odd ? v0 : v2), r1 = dpp_f<0xB1>(odd ? v1 : v3);  // lane t ^ 1
+                const int da = d0 + (odd ? 2 : 0);
+                *reinterpret_cast<uint32_t*>(wst + da * 64 + pcol) =
+                    cvt2_out<HN_DTYPE_BF16>(odd ? r0 : v0, odd ? v2 : r0);
+                *reinterpret_cast<uint32_t*>(wst + (da + 1) * 64 + pcol) =
+                    cvt2_out<HN_DTYPE_BF16>(odd ? r1 : v1, odd ? v3 : r1);
+              }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes have landed
+            __builtin_amdgcn_wave_barrier();
+            const int mb = wm * TM * 32 + j * 32;  // the block's first token (the block lies in one batch)
+            // the block's tokens and the wave's head exist (N % 128 == 0: a head is wholly inside N or past it)
+            if (mb < mrem && wn * TN * 32 < nrem) {
+              const uint32_t mg = (uint32_t)(em0 + mb);
+              const uint32_t bb = mg / (uint32_t)a.hm_L, ll = mg - bb * (uint32_t)a.hm_L;
+              const int64_t h = (en0 + wn * 128 - 2 * a.hm_hidden) / 128;
+              uint16_t* vb = a.hm_vt + bb * a.hm_svb + h * a.hm_svh + a.hm_loff + ll;
+#pragma unroll
+              for (int n = 0; n < 8; n++) {
+                const int row = n * 16 + (tl >> 2), ch = tl & 3;
+                const v4i v = *reinterpret_cast<const v4i*>(wst + row * 64 + ch * 16);
+                __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(vb + row * a.hm_svd + ch * 8));
+              }
+            }
+          } else {
           // token row (tl & 31) of this wave's staging block, then a 16-byte-per-lane write-back of the
           // block's 32 rows x TN*32 channels, non-temporal so the output stream does not evict the operand
           // panels other tiles are still reading from L2
-          char* wst = smem + STG_OFF + wave * 32 * OPITCH;
           char* ob = wst + (tl & 31) * OPITCH;
 #pragma unroll
           for (int i = 0; i < TN; i++)
@@ -1063,6 +1111,7 @@ void block_gemm_kernel(const GemmArgs a) {
                 __builtin_nontemporal_store(v, reinterpret_cast<v4i*>(obase + (uint32_t)(ml2 * (int)a.ldo + nl)));
               }
             }
+          }
           }
         } else if (m_ok) {
 #pragma unroll

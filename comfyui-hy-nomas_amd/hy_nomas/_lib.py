@@ -45,6 +45,8 @@ SIGNATURES = {
     "hn_gated_residual_frames": ([_p, _p, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p], _i),
     "hn_qkv_heads": ([_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i, _i64, _i64, _i64, _i64, _i64, _i, _p, _p,
                       _p, _p, _f, _p, _i64, _i64, _p], _i),
+    "hn_qkv_heads_vt": ([_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i, _i64, _i64, _i64, _i64, _i64, _i, _p,
+                         _p, _p, _p, _f, _p, _i64, _i64, _p, _i64, _i64, _i64, _p], _i),
     "hn_dequantize_rows": ([_p, _i64, _p, _i64, _i64, _i64, _p, _i, _i64, _p], _i),
     "hn_qk_norm_rope": ([_p, _i64, _p, _p, _p, _i64, _i64, _i64, _i64, _f, _p, _p], _i),
     "hn_pixelumm_qk": ([_p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p], _i),

@@ -59,6 +59,16 @@ def transpose_values(vh):
     return vt
 
 
+def values_buffer(b, h, lk, device, d=128):
+    """An empty V^T buffer [B, H, D, Lk padded to the key tile] for writers of the layout (`kernels.qkv_heads`
+    with `vt`): the padding keys past Lk are zeroed here, the keys themselves are left to the writer."""
+    pad = -(-lk // KEY_TILE) * KEY_TILE
+    vt = torch.empty((b, h, d, pad), device=device, dtype=torch.bfloat16)
+    if pad > lk:
+        vt[..., lk:].zero_()
+    return vt
+
+
 def _rows16(t):
     """t with a contiguous last dim and 16-byte aligned rows (a copy only when needed)."""
     if t.stride(-1) != 1 or t.data_ptr() % 16 or any(st % 8 for st in t.stride()[:-1]):

@@ -43,13 +43,14 @@ class DiTBlockInt8:
         self.per_token = per_token
         self.group = None if per_token else kernels.GROUP
 
-    def attention_heads(self, x, shift1, scale1, rope=None, out=None, l_offset=0):
+    def attention_heads(self, x, shift1, scale1, rope=None, out=None, l_offset=0, vt=None):
         """adaLN + int8 quantization -> one QKV GEMM whose epilogue applies QK-norm (+RoPE) and writes q, k, v
-        head-major: out [3, B, H, L_total, D] (tokens at l_offset ..).  x [B, L, D]."""
+        head-major: out [3, B, H, L_total, D] (tokens at l_offset ..).  x [B, L, D].  With `vt` (a V^T buffer of
+        the HIP attention), v goes there and out holds q and k."""
         b, n, d = x.shape
         qa, sa = kernels.adaln_quant(x, shift1, scale1, group=self.group)
         return kernels.qkv_heads(qa, sa, self.qkv.qw, self.qkv.sw, self.qkv.bias, self.q_norm_w, self.k_norm_w, b,
-                                 rope, out=out, l_offset=l_offset)
+                                 rope, out=out, l_offset=l_offset, vt=vt)
 
     def post(self, x, attn, gate1, shift2, scale2, gate2):
         """Out-projection + gated residual, then the MLP half with its gated residual.  attn [B, L, D]."""
@@ -94,15 +95,29 @@ class DoubleStreamBlockInt8:
         shift1, scale1, gate1, shift2, scale2, gate2 = img_mods
         tshift1, tscale1, tgate1, tshift2, tscale2, tgate2 = txt_mods
         b, lv = img.shape[0], img.shape[1]
+        heads, ltot = self.img.heads, lv + txt.shape[1]
+        whole = history is None and getattr(plan, "groups", None) is None
+        if (whole and capture is None and attn.choose_backend(backend) == "hip" and img.shape[2] == heads * 128
+                and kernels.vt_direct_ok(lv, 0) and kernels.vt_direct_ok(txt.shape[1], lv)):
+            # the HIP kernel's operands straight from the QKV epilogues: q and k head-major, v as V^T
+            hm = torch.empty((2, b, heads, ltot, 128), device=img.device, dtype=torch.bfloat16)
+            vt = attn.values_buffer(b, heads, ltot, img.device)
+            self.img.attention_heads(img, shift1, scale1, rope, out=hm, l_offset=0, vt=vt)
+            self.txt.attention_heads(txt, tshift1, tscale1, None, out=hm, l_offset=lv, vt=vt)
+            out = attn.attention_hip(hm[0].transpose(1, 2), hm[1].transpose(1, 2), vt, ltot)
+            del hm, vt
+            out = out.reshape(b, ltot, -1)
+            img = self.img.post(img, out[:, :lv], gate1, shift2, scale2, gate2)
+            txt = self.txt.post(txt, out[:, lv:], tgate1, tshift2, tscale2, tgate2)
+            return img, txt
         # both streams' q, k, v land head-major in one buffer, image tokens first (the reference's
         # torch.cat order), so attention runs on it without concatenation or layout copies
-        hm = torch.empty((3, b, self.img.heads, lv + txt.shape[1], img.shape[2] // self.img.heads),
-                         device=img.device, dtype=torch.bfloat16)
+        hm = torch.empty((3, b, heads, ltot, img.shape[2] // heads), device=img.device, dtype=torch.bfloat16)
         self.img.attention_heads(img, shift1, scale1, rope, out=hm, l_offset=0)
         self.txt.attention_heads(txt, tshift1, tscale1, None, out=hm, l_offset=lv)
         if capture is not None:
             capture(hm[1].transpose(1, 2), hm[2].transpose(1, 2))
-        if history is None and getattr(plan, "groups", None) is None:
+        if whole:
             out = attn.attention_heads(hm[0], hm[1], hm[2], backend)
         else:
             q, k, v = (t.transpose(1, 2) for t in hm)

@@ -201,13 +201,17 @@ def block_gemm(qa, sa, qw, sw, bias=None, out_dtype=torch.bfloat16, kind="int8",
 
 
 def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="int8", eps=1e-6, out=None,
-              l_offset=0):
+              l_offset=0, vt=None):
     """The q/k/v projection with QK RMSNorm and RoPE in the GEMM epilogue, written head-major for attention
     (hy_nomas/model.py:253-267 with fused.py:65-105): qa [batch * L, K] codes (scales sa), qw [3 * hidden, K]
     the stacked q, k, v weights (scales sw, bias [3 * hidden] or None), norm weights [128], rope (cos, sin)
     [L, 128] or None.  Returns `out` bf16 [3, batch, hidden / 128, L_total, 128] (allocated with
     L_total = L when not given); tokens land at rows l_offset .. l_offset + L, so the image and text streams
-    can share one buffer.  q = out[0], k = out[1], v = out[2] are contiguous [B, H, L_total, 128]."""
+    can share one buffer.  q = out[0], k = out[1], v = out[2] are contiguous [B, H, L_total, 128].
+
+    vt: a V^T buffer [batch, hidden / 128, 128, >= l_offset + L] bf16 (the HIP attention's V layout,
+    `attention.values_buffer`): v goes there instead, token l at key l_offset + l, and `out` holds only q and k
+    ([2, ...] is enough).  Needs L % 32 == 0 and l_offset % 16 == 0 (`vt_direct_ok`)."""
     _lib.require_device(qa, sa, qw, sw, bias, q_norm_w, k_norm_w)
     _check_gemm(qa, sa, qw, sw, bias, kind)
     if q_norm_w.numel() != 128 or k_norm_w.numel() != 128:
@@ -220,11 +224,23 @@ def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="
     if batch <= 0 or m % batch:
         raise RuntimeError(f"qkv_heads: {m} token rows do not split into batch {batch}")
     length = m // batch
+    parts = 3 if vt is None else 2
     if out is None:
-        out = torch.empty((3, batch, hidden // 128, length, 128), device=qa.device, dtype=torch.bfloat16)
-    if (out.dtype != torch.bfloat16 or out.dim() != 5 or tuple(out.shape[:3]) != (3, batch, hidden // 128)
-            or out.shape[4] != 128 or not out.is_contiguous() or out.shape[3] < l_offset + length):
-        raise RuntimeError(f"qkv_heads: out must be contiguous bf16 [3, {batch}, {hidden // 128}, >= {l_offset + length}, 128]")
+        out = torch.empty((parts, batch, hidden // 128, length, 128), device=qa.device, dtype=torch.bfloat16)
+    if (out.dtype != torch.bfloat16 or out.dim() != 5 or out.shape[0] < parts
+            or tuple(out.shape[1:3]) != (batch, hidden // 128) or out.shape[4] != 128 or not out.is_contiguous()
+            or out.shape[3] < l_offset + length):
+        raise RuntimeError(f"qkv_heads: out must be contiguous bf16 [{parts}, {batch}, {hidden // 128}, "
+                           f">= {l_offset + length}, 128]")
+    if vt is not None:
+        _lib.require_device(vt)
+        if not vt_direct_ok(length, l_offset):
+            raise RuntimeError(f"qkv_heads: V^T output needs L % 32 == 0 and l_offset % 16 == 0 (L={length}, "
+                               f"l_offset={l_offset})")
+        if (vt.dtype != torch.bfloat16 or vt.dim() != 4 or tuple(vt.shape[:3]) != (batch, hidden // 128, 128)
+                or vt.stride(3) != 1 or vt.shape[3] < l_offset + length):
+            raise RuntimeError(f"qkv_heads: vt must be bf16 [{batch}, {hidden // 128}, 128, >= {l_offset + length}] "
+                               "with contiguous keys")
     if m == 0:
         return out
     sw, sw_rows, group, groups = _layout(sw, n, k, kind, sa.shape[1], sa)
@@ -242,11 +258,20 @@ def qkv_heads(qa, sa, qw, sw, bias, q_norm_w, k_norm_w, batch, rope=None, kind="
         cp, sp = cos.data_ptr(), sin.data_ptr()
     else:
         cp = sp = None
-    _lib.call("hn_qkv_heads", qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
-              sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
-              batch, length, hidden, k, group, _lib.KIND[kind], wq.data_ptr(), wk.data_ptr(), cp, sp, eps,
-              out.data_ptr(), out.shape[3], l_offset, _lib.stream(qa))
+    args = (qa.data_ptr(), qa.stride(0), sa.data_ptr(), sa.stride(0), qw.data_ptr(), qw.stride(0),
+            sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0,
+            batch, length, hidden, k, group, _lib.KIND[kind], wq.data_ptr(), wk.data_ptr(), cp, sp, eps,
+            out.data_ptr(), out.shape[3], l_offset)
+    if vt is None:
+        _lib.call("hn_qkv_heads", *args, _lib.stream(qa))
+    else:
+        _lib.call("hn_qkv_heads_vt", *args, vt.data_ptr(), vt.stride(0), vt.stride(1), vt.stride(2), _lib.stream(qa))
     return out
+
+
+def vt_direct_ok(length, l_offset):
+    """Whether qkv_heads can write v of `length` tokens at key `l_offset` straight into V^T."""
+    return length % 32 == 0 and l_offset % 16 == 0
 
 
 def block_gemm_acc32(qa, qw):

@@ -150,6 +150,22 @@ int hn_qkv_heads(const void* qa, int64_t lda, const float* sa, int64_t ldsa, con
                  int64_t L_total, int64_t l_offset, void* stream);
 
 /*
+ * hn_qkv_heads with v written straight into the V^T layout hn_attention reads (its `vt`, `svb`, `svh`, `svd`),
+ * replacing the head-major v and the V^T copy the HIP attention backend would make of it (the V operand of
+ * hy_nomas/model.py:145-150 `attention`): out then holds only q and k, [2, B, hidden / 128, L_total, 128];
+ * token l of batch b lands at key l_offset + l of V^T rows b, h.  Needs L % 32 == 0, l_offset % 16 == 0, a
+ * 16-byte aligned vt, strides that are multiples of 8 with svd >= l_offset + L, svh >= 128 svd and
+ * svb >= (hidden / 128) svh.  Keys this call does not write (other streams, the padding up to a multiple of
+ * 64) are left as they are.  Other arguments and results are those of hn_qkv_heads.
+ */
+int hn_qkv_heads_vt(const void* qa, int64_t lda, const float* sa, int64_t ldsa, const void* qw, int64_t ldw,
+                    const float* sw, int64_t ldsw, int64_t sw_rows, const void* bias, int bias_dtype, int64_t B,
+                    int64_t L, int64_t hidden, int64_t K, int64_t group, int kind, const float* q_norm_w,
+                    const float* k_norm_w, const float* cos_t, const float* sin_t, float eps, void* out,
+                    int64_t L_total, int64_t l_offset, void* vt, int64_t svb, int64_t svh, int64_t svd,
+                    void* stream);
+
+/*
  * Softmax attention over all keys (no mask).  Replaces the scaled-dot-product attention of the double-stream
  * block (hy_nomas/model.py:145-150 `attention`, which hands q / k / v [B, L, H, D] to ComfyUI's backend),
  * and each query group's call in segment_attention (model.py:199-223) once the caller has gathered that

@@ -101,14 +101,17 @@ def test_segment_attention_history_and_groups(dev):
         assert fro_s < 1e-2
 
 
-@pytest.mark.parametrize("per_token", [False, True])
-def test_double_stream_block_on_the_hip_backend(dev, per_token):
-    """The double-stream block with the HIP attention kernel against the float32 block (as the SDPA run)."""
-    from hy_nomas import block
+@pytest.mark.parametrize("per_token,lv,lt", [(False, 200, 40), (True, 200, 40), (False, 224, 64), (True, 224, 64)])
+def test_double_stream_block_on_the_hip_backend(dev, per_token, lv, lt, monkeypatch):
+    """The double-stream block with the HIP attention kernel against the float32 block (as the SDPA run).  With
+    whole 32-token blocks in both streams (224 + 64) the QKV epilogues write v straight into V^T; the block's
+    output then equals, bit for bit, the run that writes v head-major and copies it to V^T."""
+    from hy_nomas import block, kernels
     from oracle import torch_forms
     from test_block_gpu import make_stream
 
-    d, heads, mlp, lv, lt = 256, 2, 1024, 200, 40
+    d, heads, mlp = 256, 2, 1024
+    print(f"double-stream block on hip per_token={per_token} {lv}+{lt}", flush=True)
     g = seeded(191 + per_token)
     img_blk = make_stream(d, heads, mlp, g, per_token, dev)
     txt_blk = make_stream(d, heads, mlp, g, per_token, dev)
@@ -116,7 +119,8 @@ def test_double_stream_block_on_the_hip_backend(dev, per_token):
     txt = torch.randn(1, lt, d, generator=g).to(torch.bfloat16).to(dev)
     img_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
     txt_mods = [(torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16).to(dev) for _ in range(6)]
-    rope = [t.to(dev) for t in torch_forms.rope_freqs([32, 48, 48], 256, 2, 10, 10)]
+    grid = (2, 10, 10) if lv == 200 else (2, 8, 14)
+    rope = [t.to(dev) for t in torch_forms.rope_freqs([32, 48, 48], 256, *grid)]
     blk = block.DoubleStreamBlockInt8(img_blk, txt_blk)
     with torch.no_grad():
         gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope, "hip")
@@ -125,6 +129,11 @@ def test_double_stream_block_on_the_hip_backend(dev, per_token):
     for got, sd, ref in ((gi, si, ri), (gt, st, rt)):
         assert rel(got, ref)[0] < 2e-2
         assert rel(got, sd)[0] < 1e-2
+    if kernels.vt_direct_ok(lv, 0) and kernels.vt_direct_ok(lt, lv):
+        monkeypatch.setattr(kernels, "vt_direct_ok", lambda *a: False)
+        with torch.no_grad():
+            ci, ct = blk.forward(img, txt, img_mods, txt_mods, rope, "hip")
+        assert torch.equal(ci, gi) and torch.equal(ct, gt)
 
 
 @pytest.mark.parametrize("backend", ["hip", "sdpa"])

@@ -73,6 +73,12 @@ def test_argument_validation_without_a_gpu():
     rc = l.hn_qkv_heads(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 1, 64, 256, 256, 128, 0, None, None,
                         None, None, 1e-6, None, 70, 10, None)  # tokens [10, 74) past L_total 70
     assert rc == 1 and b"L_total" in l.hn_last_error()
+    rc = l.hn_qkv_heads_vt(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 1, 48, 256, 256, 128, 0, None, None,
+                           None, None, 1e-6, None, 64, 0, 16, 128 * 64 * 2, 128 * 64, 64, None)   # L = 48
+    assert rc == 1 and b"multiple of 32" in l.hn_last_error()
+    rc = l.hn_qkv_heads_vt(None, 256, None, 2, None, 256, None, 2, 1, None, 0, 1, 64, 256, 256, 128, 0, None, None,
+                           None, None, 1e-6, None, 64, 0, 16, 128 * 32 * 2, 128 * 32, 32, None)   # rows of 32 keys < 64
+    assert rc == 1 and b"V^T strides" in l.hn_last_error()
     rc = l.hn_gated_residual_frames(None, None, None, None, 0, 1, 2, 3, 100, None, None)   # D % 8 != 0
     assert rc == 1 and b"multiple of 8" in l.hn_last_error()
     rc = l.hn_block_gemm(None, 131072, None, 1, None, 131072, None, 1, 1, None, 0, 4, 8, 131072, 131072, 0, 0, None,

@@ -88,3 +88,43 @@ def test_qkv_heads_two_streams_share_one_buffer(dev):
     assert torch.equal(alone_t[2, 0], v_t)
     with pytest.raises(RuntimeError):
         kernels.qkv_heads(qt, st, wt, sblk, None, wq, wk, 1, None, kind="fp8", out=hm, l_offset=li + 1)
+
+
+@pytest.mark.parametrize("layout", ["g128", "per_token"])
+def test_qkv_heads_vt_matches_head_major(dev, layout):
+    """v written straight into the HIP attention's V^T layout (hn_qkv_heads_vt): equal bit for bit to the V^T
+    copy of the head-major v (attention.transpose_values), q and k to the head-major call's; two streams at
+    their key offsets (an image stream of 2 x 320 tokens, then 32 text tokens with fp8 block scales), hidden
+    384 (a tile holding a k head and a v head), the padding keys up to 384 left as they were."""
+    from hy_nomas import attention, kernels, pixelumm
+
+    print(f"qkv_heads V^T {layout}", flush=True)
+    g = seeded(31)
+    hidden, k, b, li, lt = 384, 256, 2, 320, 32
+    ltot = li + lt
+    xi = torch.randn(b * li, k, generator=g).to(torch.bfloat16).to(dev)
+    xt = torch.randn(b * lt, k, generator=g).to(torch.bfloat16).to(dev)
+    qi, si = kernels.quantize_activations(xi, "int8", None if layout == "per_token" else 128)
+    wi, swi, bi = make_qkv(g, hidden, k, layout, dev)
+    qt, st = kernels.quantize_activations(xt, "fp8")
+    wt, sblk = pixelumm.quantize_fp8_block(torch.randn(3 * hidden, k, generator=g) * 0.02)
+    wt, sblk = wt.to(dev), sblk.to(dev)
+    wq = (torch.rand(128, generator=g) + 0.5).to(dev)
+    wk = (torch.rand(128, generator=g) + 0.5).to(dev)
+    rope = tuple(t.to(dev) for t in rope_tables(g, li))
+    hm = torch.empty((3, b, hidden // 128, ltot, 128), device=dev, dtype=torch.bfloat16)
+    kernels.qkv_heads(qi, si, wi, swi, bi, wq, wk, b, rope, out=hm, l_offset=0)
+    kernels.qkv_heads(qt, st, wt, sblk, None, wq, wk, b, None, kind="fp8", out=hm, l_offset=li)
+    vt_ref = attention.transpose_values(hm[2])
+    qk = torch.full((2, b, hidden // 128, ltot, 128), float("nan"), device=dev, dtype=torch.bfloat16)
+    vt = torch.full(tuple(vt_ref.shape), float("nan"), device=dev, dtype=torch.bfloat16)
+    kernels.qkv_heads(qi, si, wi, swi, bi, wq, wk, b, rope, out=qk, l_offset=0, vt=vt)
+    assert torch.isnan(vt[..., li:].float()).all()          # the text keys are not this call's
+    kernels.qkv_heads(qt, st, wt, sblk, None, wq, wk, b, None, kind="fp8", out=qk, l_offset=li, vt=vt)
+    assert torch.equal(qk, hm[:2])
+    assert torch.equal(vt[..., :ltot], vt_ref[..., :ltot])
+    assert vt.shape[3] == 384 and torch.isnan(vt[..., ltot:].float()).all()   # padding keys untouched
+    pad = attention.values_buffer(b, hidden // 128, ltot, dev)
+    assert pad.shape == vt_ref.shape and not pad[..., ltot:].any()
+    with pytest.raises(RuntimeError):                       # 36 tokens: not whole 32-token blocks
+        kernels.qkv_heads(qt[:36], st[:36], wt, sblk, None, wq, wk, 1, None, kind="fp8", l_offset=li, vt=vt)
