@@ -69,10 +69,11 @@ def make_linear_on(dev, gen, n, k, per_channel):
     return block.Int8Linear(qw, sw.float(), bias)
 
 
-@pytest.mark.parametrize("per_token", [True, False])
-def test_double_stream_block_full_size(dev, per_token):
+@pytest.mark.parametrize("per_token,backend", [(True, "sdpa"), (False, "sdpa"), (True, "hip"), (False, "hip")])
+def test_double_stream_block_full_size(dev, per_token, backend):
     """The config-4 block at its real size: hidden 3072, 24 heads x 128, FFN 12288, 57344 image tokens on a
-    14 x 64 x 64 RoPE grid plus 256 text tokens, both activation layouts.  The float32 reference (dequantized
+    14 x 64 x 64 RoPE grid plus 256 text tokens, both activation layouts, both attention backends (the HIP one
+    with v written straight into its V^T layout by the QKV epilogues).  The float32 reference (dequantized
     weights, unquantized activations, hy_nomas/model.py:230-303) computes q/k/v for every token and the
     attention and row-local rest of the block for sampled rows of each stream; the int8 block's rows must
     match within 2e-2 relative (as the small-block test), and so must the block's change to the stream."""
@@ -80,7 +81,7 @@ def test_double_stream_block_full_size(dev, per_token):
     from oracle import torch_forms
 
     d, heads, mlp, lv, lt = 3072, 24, 12288, 57344, 256
-    print(f"double-stream block full size per_token={per_token} ({lv}+{lt} tokens)", flush=True)
+    print(f"double-stream block full size per_token={per_token} backend={backend} ({lv}+{lt} tokens)", flush=True)
     gen = torch.Generator(device=dev).manual_seed(2024 + per_token)
 
     def stream():
@@ -97,7 +98,7 @@ def test_double_stream_block_full_size(dev, per_token):
     rope = torch_forms.rope_freqs([16, 56, 56], 256, 14, 64, 64, device=dev)
     blk = block.DoubleStreamBlockInt8(img_blk, txt_blk)
     with torch.no_grad():
-        gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope)
+        gi, gt = blk.forward(img, txt, img_mods, txt_mods, rope, backend)
         torch.cuda.synchronize()
         g = seeded(55 + per_token)
         img_rows = sorted(set(torch.randperm(lv, generator=g)[:30].tolist() + [0, lv - 1]))
