@@ -101,10 +101,6 @@ __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) 
   return ((const float*)bias)[n];
 }
 
-// torch's silu of a bf16 value, computed in fp32 as x / (1 + exp(-x)) (the reference's F.silu,
-// hy_nomas/pixelumm.py:322, on a bf16 tensor)
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
-
 __device__ __forceinline__ float gelu_tanh(float x) {
   // kernels.py:74-77 in fp32, in the order written, with sigmoid(2 inner) = 1 / (1 + exp(-2 inner)) taken
   // from the hardware base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32: about 1 ulp each).  The
@@ -878,7 +874,7 @@ void block_gemm_kernel(const GemmArgs a) {
                 const float other = __uint_as_float((e & 1) ? (pw & 0xffff0000u) : (pw << 16));
                 const float own = MF::get(acc[i][J0 + jj], r);
                 const float g = OWN_GATE ? own : other, u = OWN_GATE ? other : own;
-                const float hv = rbf16(rbf16(silu_f32(g)) * u);
+                const float hv = rbf16(silu_bf16(g) * u);
                 MF::put(acc[i][J0 + jj], r, hv);
                 peak = __builtin_fmaxf(peak, __builtin_fabsf(hv));
               }

@@ -47,6 +47,23 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// torch's silu of a bf16 value, computed in fp32 as x / (1 + exp(-x)) (the reference's F.silu,
+// hy_nomas/pixelumm.py:322, on a bf16 tensor).
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+// rbf16(silu_f32(g)) for a g that is a bf16 value, from the hardware base-2 exponential and reciprocal
+// (v_exp_f32, v_rcp_f32).  For g >= -16 that value is within about 20 fp32 ulps of silu_f32(g) (the
+// exponential's input carries |g| log2(e) 2^-24 of relative error), so both round to the same bf16 value
+// unless it lies within 32 ulps of a rounding midpoint; such lanes, g < -16 and non-finite g take silu_f32.
+// Exhaustively equal to rbf16(silu_f32(g)) for all 65536 bf16 g (libhynomas_probes.so: hnp_silu_mismatches).
+__device__ __forceinline__ float silu_bf16(float g) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  const float f = g * __builtin_amdgcn_rcpf(1.0f + e);
+  const uint32_t low = __float_as_uint(f) & 0xffffu;
+  if (__builtin_expect((low - 0x7fe0u) < 0x40u || !(g >= -16.0f), 0)) return rbf16(silu_f32(g));
+  return rbf16(f);
+}
+
 // OCP e4m3fn encoding, round to nearest even; values that round past 448 give the NaN code 0x7F.
 __device__ __forceinline__ uint32_t e4m3_encode(float f) {
   uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;

@@ -124,3 +124,27 @@ def test_swiglu_quant_rejects_bad_layouts(dev):
     w = kernels.quantize_activations(torch.randn(256, 256, generator=g).to(dev), "int8")
     with pytest.raises(RuntimeError):                # int8 g128: no two-token-block tile for the split
         kernels.block_gemm(qi, si, w[0], w[1], kind="int8", epilogue="swiglu_quant")
+
+
+def test_fast_silu_equals_the_reference_for_every_bf16_value(dev):
+    """The SwiGLU epilogue's silu of a bf16 value (hardware exponential and reciprocal, the library form near
+    bf16 rounding midpoints and for g < -16) against the fp32 form rounded to bf16, for all 65536 bf16 bit
+    patterns (libhynomas_probes.so: hnp_silu_mismatches), and against torch's silu of the bf16 values on the
+    CPU (the reference's F.silu), NaNs compared as NaNs."""
+    import ctypes
+    import os
+
+    path = os.path.join(os.path.dirname(__file__), "..", "comfyui-hy-nomas_amd", "hy_nomas", "libhynomas_probes.so")
+    lib = ctypes.CDLL(path)
+    lib.hnp_silu_mismatches.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    value = torch.empty(65536, dtype=torch.int32, device=dev)
+    bad = torch.empty(65536, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.hnp_silu_mismatches(value.data_ptr(), bad.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(bad.sum().item()) == 0
+    g = (torch.arange(65536, dtype=torch.int32) << 16).view(torch.float32).to(torch.bfloat16)
+    ref = torch.nn.functional.silu(g).float()
+    got = value.cpu().view(torch.float32)
+    both_nan = torch.isnan(ref) & torch.isnan(got)
+    assert torch.equal(got[~both_nan], ref[~both_nan])
