@@ -99,6 +99,36 @@ def test_int8_gemm_bit_exact(dev, m, n, k, per_channel, with_bias):
     assert max_abs_rel(got.float().numpy(), fp64_dequant_product(qa, sa, w.numpy(), sw.numpy(), bias)) < 1e-2
 
 
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_int8_gemm_signed_zeros(dev, with_bias):
+    """Exact-zero dot products (all-zero token rows and weight rows) under negative channel scales, with
+    biases of -0 and +0: the output bits, the signs of zeros included, are the oracle's
+    ((0 + (x sa) sw) + b in fp32, then bf16), for per-token scales and for the g128 layout."""
+    from hy_nomas import kernels
+
+    print(f"int8 gemm signed zeros bias={with_bias}", flush=True)
+    m, n, k = 96, 256, 512
+    x = outlier_input(m, k, seed=77)
+    x[::7] = 0
+    for per_channel in (True, False):
+        w, sw, bias = int8_weights(n, k, seed=78, per_channel=per_channel)
+        w[::5] = 0
+        sw[::3] = -sw[::3]
+        bias[::2] = -0.0
+        bias[1::4] = 0.0
+        bias = bias if with_bias else None
+        qa, sa = oracle.quantize(x, k if per_channel else 128)
+        out = kernels.block_gemm(torch.from_numpy(qa).to(dev), torch.from_numpy(sa).to(dev), w.to(dev), sw.to(dev),
+                                 bias.to(dev) if bias is not None else None)
+        ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias) if bias is not None else None)
+        want = torch.from_numpy(ref).to(torch.bfloat16).view(torch.int16)
+        got = out.cpu().view(torch.int16)
+        # zero products in channels with sw < 0 and b = -0 (or no bias): a plain (x sa) sw + b gives -0 there
+        assert (want == 0).any() and not (want == -32768).any()
+        diff = (got != want).nonzero()
+        assert diff.numel() == 0, f"per_channel={per_channel}: {len(diff)} output bit patterns differ, first {diff[:3].tolist()}"
+
+
 @pytest.mark.parametrize("m,n,k,epilogue", [
     (64, 288, 256, None), (300, 1000, 384, None), (513, 520, 640, None), (40, 4096, 256, None),
     (130, 384, 384, None), (40, 4096, 256, "gelu_quant"), (130, 384, 384, "gelu_quant")])
