@@ -158,14 +158,28 @@ void attention_kernel(const AttnArgs a) {
 
     // S^T for the tile's two 32-key blocks (interleaved): lane holds query l32, keys 32 kb + 8 (r / 4) + 4 h2 + r % 4
     v16f_a s[2];
+    // the K fragments two steps ahead of their products (a ring of three), so each read has two steps of
+    // products to land in
+    bf16x8 kf[3][2];
+    auto read_k = [&](int ks, bf16x8* f) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++)
+      for (int kb = 0; kb < 2; kb++)
+        f[kb] = *reinterpret_cast<const bf16x8*>(kt + (32 * kb + l32) * 256 + (((2 * ks + h2) ^ kswz) << 4));
+    };
+    read_k(0, kf[0]);
+    read_k(1, kf[1]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        const bf16x8 af =
-            *reinterpret_cast<const bf16x8*>(kt + (32 * kb + l32) * 256 + (((2 * ks + h2) ^ kswz) << 4));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[ks], ks == 0 ? mref : s[kb], 0, 0, 0);
+    for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3][kb], qf[ks], ks == 0 ? mref : s[kb], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      if (ks + 2 < 8) {
+        read_k(ks + 2, kf[(ks + 2) % 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
+    }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
       // register r of block kb holds key j0 + 32 kb + 8 (r / 4) + (r % 4) + 4 h2: a constant per register
       // against one per-lane limit
