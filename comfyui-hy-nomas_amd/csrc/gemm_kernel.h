@@ -100,6 +100,15 @@ __device__ __forceinline__ float load_bias(const void* bias, int dt, int64_t n) 
   if (dt == HN_DTYPE_F16) return f16_bits_to_f32(((const uint16_t*)bias)[n]);
   return ((const float*)bias)[n];
 }
+// the same in two steps: the element's bits (no use of the loaded value, so no wait for it), then the value
+__device__ __forceinline__ uint32_t load_bias_bits(const void* bias, int dt, int64_t n) {
+  return dt == HN_DTYPE_F32 ? ((const uint32_t*)bias)[n] : (uint32_t)((const uint16_t*)bias)[n];
+}
+__device__ __forceinline__ float bias_from_bits(uint32_t b, int dt) {
+  if (dt == HN_DTYPE_BF16) return bf16_bits_to_f32(b);
+  if (dt == HN_DTYPE_F16) return f16_bits_to_f32(b);
+  return __uint_as_float(b);
+}
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   // kernels.py:74-77 in fp32, in the order written, with sigmoid(2 inner) = 1 / (1 + exp(-2 inner)) taken
@@ -278,7 +287,9 @@ void block_gemm_kernel(const GemmArgs a) {
   constexpr int STG_END = STG_OFF + STG_BYTES;
   constexpr int EP_OFF = STG_END > RING_END ? STG_END : RING_END;
   constexpr int EP_BYTES = EPI == HN_EPI_ACC32 ? 0 : (2 * BN + BM) * 4;  // sw | bias | sa of the tile
-  constexpr int SMEM = EP_OFF + EP_BYTES > RING_END ? EP_OFF + EP_BYTES : RING_END;
+  // (two operand buffers when the next tile's are parked before this tile's epilogue)
+  constexpr int EP_BUFS = STAGED && !G128 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU) ? 2 : 1;
+  constexpr int SMEM = EP_OFF + EP_BUFS * EP_BYTES > RING_END ? EP_OFF + EP_BUFS * EP_BYTES : RING_END;
   __shared__ __align__(16) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -418,9 +429,64 @@ void block_gemm_kernel(const GemmArgs a) {
   static_assert(!BMAJ || TM >= 2, "the weight fragments of the next channel block are read during the last token block");
   Frag fbs[BMAJ ? TM : 1][BMAJ ? SLICES : 1], fas[BMAJ ? SLICES : 1];
 
+  // The tile's epilogue operands (per-channel weight scale and bias, per-token activation scale), parked in
+  // LDS for the epilogue.  Rows and channels past the edge take the last valid one; an absent bias reads as
+  // -0.0, which leaves every sum (signed zeros included) unchanged.  Most epilogues fetch them at the tile
+  // top, where their latency overlaps the wait for stage 0.  The plain staged per-token epilogues
+  // (EARLY_EP) fetch the next tile's before the last stage of this one and park them in the other of two
+  // operand buffers before this tile's epilogue, so no load into registers is pending when that epilogue's
+  // stores are issued: the next tile top then waits for its first stage alone and leaves the stores (the
+  // youngest vector-memory ops; the counter retires in issue order) in flight under its first products.
+  constexpr int EP_PER = EPI == HN_EPI_ACC32 ? 0 : (BN + NW * 64 - 1) / (NW * 64);
+  constexpr int EPM_PER = EPI == HN_EPI_ACC32 || G128 ? 0 : (BM + NW * 64 - 1) / (NW * 64);
+  constexpr bool EARLY_EP = STAGED && !G128 && (EPI == HN_EPI_NONE || EPI == HN_EPI_GELU);
+  constexpr int NST = TM * 32 / (64 / (TN * 32 * 2 / 16));  // the staged epilogue's stores per full tile
+  static_assert(NST < 64, "vmcnt range");
+  float ep_sw[EP_PER > 0 ? EP_PER : 1], ep_b[EP_PER > 0 ? EP_PER : 1], ep_sa[EPM_PER > 0 ? EPM_PER : 1];
+  uint32_t ep_bb[EP_PER > 0 ? EP_PER : 1];  // EARLY_EP: the bias bits (-0.0 when absent), converted when parked
+  auto fetch_ep = [&](int64_t tm0, int64_t tn0) __attribute__((always_inline)) {
+    const int64_t nleft0 = a.N - tn0, mleft0 = a.M - tm0;
+    const int nlast = nleft0 < BN ? (int)nleft0 - 1 : BN - 1, mlast = mleft0 < BM ? (int)mleft0 - 1 : BM - 1;
+#pragma unroll
+    for (int u = 0; u < EP_PER; u++) {
+      const int tt = tid + u * NW * 64;
+      const int64_t n = tn0 + (tt < nlast ? tt : nlast);
+      ep_sw[u] = G128 ? 0.0f : a.sw[n * a.ldsw];
+      if constexpr (EARLY_EP) ep_bb[u] = a.bias ? load_bias_bits(a.bias, a.bias_dtype, n) : 0x80000000u;
+      else ep_b[u] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : -0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < EPM_PER; u++) {
+      const int tt = tid + u * NW * 64;
+      ep_sa[u] = a.sa[(tm0 + (tt < mlast ? tt : mlast)) * a.ldsa];
+    }
+  };
+  auto write_ep = [&](int buf) __attribute__((always_inline)) {
+    if constexpr (EPI != HN_EPI_ACC32) {
+      float* ep = reinterpret_cast<float*>(smem + EP_OFF + buf * EP_BYTES);
+#pragma unroll
+      for (int u = 0; u < EP_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        const float b = EARLY_EP ? (a.bias ? bias_from_bits(ep_bb[u], a.bias_dtype) : -0.0f) : ep_b[u];
+        if (tt < BN) { ep[tt] = ep_sw[u]; ep[BN + tt] = b; }
+      }
+#pragma unroll
+      for (int u = 0; u < EPM_PER; u++) {
+        const int tt = tid + u * NW * 64;
+        if (tt < BM) ep[2 * BN + tt] = ep_sa[u];
+      }
+    }
+  };
+  bool stores_full = false;  // EARLY_EP: the previous tile's epilogue issued all NST of its stores
+  int epb = 0;               // EARLY_EP: the operand buffer of the current tile
+
   int64_t m0, n0;
   tile_origin(t, m0, n0);
   plan_loads(m0, n0, lane);
+  if constexpr (EARLY_EP) {  // the first tile's operands (published by the first tile-top barrier)
+    fetch_ep(m0, n0);
+    write_ep(0);
+  }
   issue_stage(0, 0);
 
   for (;;) {
@@ -447,47 +513,16 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; r++) facc[i][j][r] = 0.0f;
     }
-    // The tile's epilogue operands (per-channel weight scale and bias, per-token activation scale) are
-    // fetched here, so their latency overlaps the wait for stage 0, and parked in LDS for the epilogue.
-    // Rows and channels past the edge take the last valid one; an absent bias reads as -0.0, which
-    // leaves every sum (signed zeros included) unchanged.
-    constexpr int EP_PER = EPI == HN_EPI_ACC32 ? 0 : (BN + NW * 64 - 1) / (NW * 64);
-    constexpr int EPM_PER = EPI == HN_EPI_ACC32 || G128 ? 0 : (BM + NW * 64 - 1) / (NW * 64);
-    float ep_sw[EP_PER > 0 ? EP_PER : 1], ep_b[EP_PER > 0 ? EP_PER : 1], ep_sa[EPM_PER > 0 ? EPM_PER : 1];
-    {
-      const int64_t nleft0 = a.N - n0, mleft0 = a.M - m0;
-      const int nlast = nleft0 < BN ? (int)nleft0 - 1 : BN - 1, mlast = mleft0 < BM ? (int)mleft0 - 1 : BM - 1;
-#pragma unroll
-      for (int u = 0; u < EP_PER; u++) {
-        const int tt = tid + u * NW * 64;
-        const int64_t n = n0 + (tt < nlast ? tt : nlast);
-        ep_sw[u] = G128 ? 0.0f : a.sw[n * a.ldsw];
-        ep_b[u] = a.bias ? load_bias(a.bias, a.bias_dtype, n) : -0.0f;
-      }
-#pragma unroll
-      for (int u = 0; u < EPM_PER; u++) {
-        const int tt = tid + u * NW * 64;
-        ep_sa[u] = a.sa[(m0 + (tt < mlast ? tt : mlast)) * a.ldsa];
-      }
-    }
-    // stage 0 has landed (this also retires the previous tile's stores) and every wave's staging and
-    // operand reads of the previous epilogue are done, so buffer 1 and the operand area are free
-    wait_vmcnt<0>();
+    if constexpr (!EARLY_EP) fetch_ep(m0, n0);
+    // stage 0 (and the epilogue operands) have landed and every wave's staging and operand reads of the
+    // previous epilogue are done, so buffer 1 and the operand area are free.  After a full tile of a plain
+    // staged epilogue its NST stores are the youngest vector-memory ops and may still be in flight (the
+    // counter retires in issue order); otherwise this also retires the previous tile's stores.
+    if (EARLY_EP && stores_full) wait_vmcnt<NST>();
+    else wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     barrier();
-    if constexpr (EPI != HN_EPI_ACC32) {
-      float* ep = reinterpret_cast<float*>(smem + EP_OFF);
-#pragma unroll
-      for (int u = 0; u < EP_PER; u++) {
-        const int tt = tid + u * NW * 64;
-        if (tt < BN) { ep[tt] = ep_sw[u]; ep[BN + tt] = ep_b[u]; }
-      }
-#pragma unroll
-      for (int u = 0; u < EPM_PER; u++) {
-        const int tt = tid + u * NW * 64;
-        if (tt < BM) ep[2 * BN + tt] = ep_sa[u];
-      }
-    }
+    if constexpr (!EARLY_EP) write_ep(0);
     if (1 < nk) issue_stage(1, 1);
     if constexpr (BMAJ) {
 #pragma unroll
@@ -758,6 +793,13 @@ void block_gemm_kernel(const GemmArgs a) {
         stage_body(kt, kt & 1, std::integral_constant<int, 1>());
         kt++;
       }
+      if constexpr (EARLY_EP) {  // the next tile's epilogue operands land during the last stage
+        if (t + nwx < t_end) {
+          int64_t nm0, nn0;
+          tile_origin(t + nwx, nm0, nn0);
+          fetch_ep(nm0, nn0);
+        }
+      }
       stage_body(kt, kt & 1, std::integral_constant<int, 2>());
     }
     // every wave is done reading the stage buffers (and the scale ring) of this tile
@@ -773,6 +815,7 @@ void block_gemm_kernel(const GemmArgs a) {
       plan_loads(m0, n0, tl);
       krev = !krev;
       issue_stage(0, 0);
+      if constexpr (EARLY_EP) write_ep(epb ^ 1);  // its last reader was the previous epilogue
     }
     if constexpr (BMAJ) {  // the last group's last block, while the next tile's first stage lands
       fold_chunk(facc[TN - 1][TM - 1], part[(TN * TM - 1) & 1], c_sa[TM - 1], c_sw[TN - 1],
@@ -784,6 +827,7 @@ void block_gemm_kernel(const GemmArgs a) {
     // rows ml < mrem and channels nl < nrem exist.
     const int64_t mleft = a.M - em0, nleft = a.N - en0;
     const int mrem = mleft < BM ? (int)mleft : BM, nrem = nleft < BN ? (int)nleft : BN;
+    stores_full = mrem == BM && nrem == BN;
     const int nloc = wn * TN * 32 + (tl >> 5) * 4;
     const int erow_m = wm * TM * 32 + (tl & 31);
     if constexpr (EPI == HN_EPI_ACC32) {
@@ -803,7 +847,7 @@ void block_gemm_kernel(const GemmArgs a) {
       }
     } else if constexpr (EPI == HN_EPI_SWIGLU_QUANT) {
       // per-channel bias and per-token scale of this tile (written at the tile top)
-      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF);
+      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF + (EARLY_EP ? epb * EP_BYTES : 0));
       constexpr int JH = TM / 2;
       // every output of the wave to its bf16 value: gate_proj(x) on wave wn = 0, up_proj(x) on wn = 1
 #pragma unroll
@@ -917,7 +961,7 @@ void block_gemm_kernel(const GemmArgs a) {
       else finish(std::integral_constant<int, JH>(), std::false_type());
     } else {
       // per-channel scale and bias, and per-token scale, of this tile (written at the tile top)
-      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF);
+      const float* ep = reinterpret_cast<const float*>(smem + EP_OFF + (EARLY_EP ? epb * EP_BYTES : 0));
 #pragma unroll
       for (int j = 0; j < TM; j++) {
         const int ml = erow_m + j * 32;
@@ -1143,6 +1187,7 @@ void block_gemm_kernel(const GemmArgs a) {
         }
       }
     }
+    if constexpr (EARLY_EP) epb ^= 1;
     if (!more) break;
     // the next tile's load offsets again (recomputed rather than kept live across the epilogue)
     int tl2 = lane;
