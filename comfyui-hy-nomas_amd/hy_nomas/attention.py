@@ -61,11 +61,17 @@ def transpose_values(vh):
 
 def values_buffer(b, h, lk, device, d=128):
     """An empty V^T buffer [B, H, D, Lk padded to the key tile] for writers of the layout (`kernels.qkv_heads`
-    with `vt`): the padding keys past Lk are zeroed here, the keys themselves are left to the writer."""
+    with `vt`): the padding keys past Lk are zeroed here, the keys themselves are left to the writer.
+
+    Keys are permuted within each 16-key group, so when Lk % 16 != 0 some padding keys of the last partial
+    group sit at physical positions below Lk.  The zeroing therefore starts at that group's first position;
+    the writer then overwrites the group's real keys.  (The kernel gives padding keys zero weight, but a
+    zero weight times uninitialised NaN bits would still be NaN.)"""
     pad = -(-lk // KEY_TILE) * KEY_TILE
     vt = torch.empty((b, h, d, pad), device=device, dtype=torch.bfloat16)
-    if pad > lk:
-        vt[..., lk:].zero_()
+    start = lk // 16 * 16
+    if pad > start:
+        vt[..., start:].zero_()
     return vt
 
 

@@ -228,6 +228,21 @@ def test_attention_backend_selection_and_value_layout(monkeypatch):
         assert torch.equal(vt[..., pos], vh.transpose(-1, -2))
         rest = sorted(set(range(pad)) - set(pos))
         assert not vt[..., rest].any()
+    # values_buffer for writers that fill only the real keys: every padding key is zero, including those of a
+    # partial last 16-key group that the grouped order places below Lk.  torch.empty is made to return NaN
+    # bits, so that memory which happens to be zero cannot hide a position the buffer leaves uninitialised.
+    real_empty = torch.empty
+    for lk in (70, 64, 37, 5, 130, 16):
+        with monkeypatch.context() as mp:
+            mp.setattr(torch, "empty", lambda *a, **kw: real_empty(*a, **kw).fill_(float("nan")))
+            buf = attention.values_buffer(2, 3, lk, "cpu")
+        pad = -(-lk // 64) * 64
+        assert buf.shape == (2, 3, 128, pad)
+        pos = [16 * (j // 16) + 8 * ((j // 4) % 2) + 4 * ((j // 8) % 2) + j % 4 for j in range(lk)]
+        rest = sorted(set(range(pad)) - set(pos))
+        assert not buf[..., rest].any(), f"lk={lk}: padding keys left uninitialised"
+        if lk % 16 > 4:
+            assert min(rest) < lk  # the case the grouped order creates
     # a token-major value tensor viewed head-major (the layout attention() passes)
     v = torch.randn(1, 40, 2, 128).to(torch.bfloat16)
     assert torch.equal(attention.transpose_values(v.transpose(1, 2)), attention.transpose_values(v.transpose(1, 2).contiguous()))
