@@ -120,7 +120,9 @@ int hn_block_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * Arguments and results are those of hn_block_linear; a problem needing more than
  * HN_NOALLOC_SCRATCH_BYTES (hn_block_linear_workspace_bytes(M, K, group)) is rejected with HN_ERR_ARG.
  * All calls on one GPU share its array: calls that overlap on one GPU (other streams or threads) race,
- * and must be serialized by the caller.
+ * and must be serialized by the caller.  The first call on each device looks up the array's device address
+ * (hipGetSymbolAddress); callers that capture the call into a HIP graph make one call on that device before
+ * capturing.  The captured call records kernel launches only (no memset, copy or allocation).
  */
 #define HN_NOALLOC_SCRATCH_BYTES (32LL << 20)
 

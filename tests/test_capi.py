@@ -109,3 +109,30 @@ def test_attention_argument_validation_without_a_gpu():
     assert call(skj=1 << 24) == 1 and b"out of range" in l.hn_last_error()
     assert call(scale=0.0) == 1 and b"scale" in l.hn_last_error()
     assert call(Lk=0) == 1 and b"bad shape" in l.hn_last_error()
+
+
+def test_noalloc_rejects_problems_beyond_the_scratch():
+    """hn_block_linear_noalloc refuses, before any HIP call, a problem whose codes and scales exceed the scratch
+    array the header declares.  The size is read from the header, so a larger array keeps the case out of
+    range.  Runs only where no GPU is visible: the pointers passed are placeholders."""
+    import torch
+    from hy_nomas import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhynomas_hip.so not built")
+    if torch.cuda.is_available():
+        pytest.skip("placeholder pointers: host-only check")
+    text = open(HEADER).read()
+    scratch = eval(re.search(r"#define HN_NOALLOC_SCRATCH_BYTES\s+\(([^)]*)\)", text).group(1).replace("LL", ""))
+    l = _lib.lib()
+    k = 3072
+    m = scratch // k + 1
+    assert l.hn_block_linear_workspace_bytes(m, k, 128) > scratch
+    assert l.hn_block_linear_workspace_bytes(m, k, k) > scratch
+    for group in (128, k):
+        rc = l.hn_block_linear_noalloc(1 << 20, 0, k, m, k, group, 0, 0, 1 << 20, k, 1 << 20, k // 128, 1, None, 0,
+                                       256, 1 << 20, 0, 256, None)
+        assert rc == 1 and b"scratch" in l.hn_last_error()
+    # and a problem just inside the array is within the limit
+    fits = scratch // (k + 4 * (k // 128)) - 1
+    assert 0 < l.hn_block_linear_workspace_bytes(fits, k, 128) <= scratch

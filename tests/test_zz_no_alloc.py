@@ -1,6 +1,7 @@
 """hn_block_linear_noalloc (the one-call linear on the library's own scratch array) against hn_block_linear (the
 same linear on a caller workspace): identical outputs on consecutive calls, the later ones smaller, across the
-scale layouts; problems beyond the scratch size are rejected before any launch."""
+scale layouts, and under HIP graph capture.  (Problems beyond the scratch size are rejected before any launch:
+tests/test_capi.py checks that on the CPU.)"""
 import pytest
 import torch
 
@@ -9,12 +10,13 @@ from conftest import seeded
 pytestmark = pytest.mark.gpu
 
 
-def noalloc(x, qw, sw, bias, group, kind, sw_rows=1, rounding="half_away"):
+def noalloc(x, qw, sw, bias, group, kind, sw_rows=1, rounding="half_away", out=None):
     from hy_nomas import _lib
 
     m, k = x.shape
     n = qw.shape[0]
-    out = torch.empty((m, n), device=x.device, dtype=x.dtype)
+    if out is None:
+        out = torch.empty((m, n), device=x.device, dtype=x.dtype)
     _lib.call("hn_block_linear_noalloc", x.data_ptr(), _lib.dtype_code(x), x.stride(0), m, k, group, _lib.KIND[kind],
               _lib.ROUND[rounding], qw.data_ptr(), qw.stride(0), sw.data_ptr(), sw.stride(0), sw_rows, _lib.ptr(bias),
               _lib.dtype_code(bias) if bias is not None else 0, n, out.data_ptr(), _lib.dtype_code(out), out.stride(0),
@@ -76,12 +78,26 @@ def test_noalloc_rounding_and_repeat(dev):
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
-def test_noalloc_rejects_problems_beyond_the_scratch(dev):
-    from hy_nomas import _lib
-
-    l = _lib.lib()
-    m, k = 16384, 3072   # 50 MB of codes and scales
-    assert l.hn_block_linear_workspace_bytes(m, k, 128) > 32 << 20
-    rc = l.hn_block_linear_noalloc(1 << 20, 0, k, m, k, 128, 0, 0, 1 << 20, k, 1 << 20, k // 128, 1, None, 0, 256,
-                                   1 << 20, 0, 256, None)
-    assert rc == 1 and b"scratch" in l.hn_last_error()
+def test_noalloc_under_graph_capture(dev):
+    """The entry point inside a captured HIP graph: one call outside capture first (the first call on a device
+    looks up the scratch array's address), then the call captured once and replayed on fresh inputs, with
+    eager work and synchronizations between the replays; every replay equals the workspace entry point."""
+    print("hn_block_linear_noalloc under graph capture", flush=True)
+    g = seeded(4098)
+    for layout in ("int8_g128", "int8_per_token", "fp8_block"):
+        x, qw, sw, bias, group, kind, sw_rows = case(dev, g, 640, 1024, 768, layout)
+        out = torch.empty((x.shape[0], qw.shape[0]), device=dev, dtype=x.dtype)
+        noalloc(x, qw, sw, bias, group, kind, sw_rows, out=out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            noalloc(x, qw, sw, bias, group, kind, sw_rows, out=out)
+        torch.cuda.synchronize()
+        for replay in range(3):
+            x.copy_((torch.randn(x.shape, generator=g) * (replay + 1)).to(torch.bfloat16))
+            graph.replay()
+            torch.cuda.synchronize()
+            ref = with_workspace(x, qw, sw, bias, group, kind, sw_rows)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"{layout}: replay {replay} differs from the eager call"
+            assert out.abs().max().item() > 0
