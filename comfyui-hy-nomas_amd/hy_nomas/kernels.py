@@ -23,9 +23,12 @@ EPILOGUES = {None: 0, "gelu": 1, "gelu_quant": 2, "swiglu_quant": 4}
 # K < 131072.  Longer K takes the per-group fold with the single scale repeated per group.
 WHOLE_K_INT32_LIMIT = 131072
 
-# Scale tensors already known to be positive and finite (or not), by tensor identity and in-place
-# version: {id: (weakref, version, ok)}.  The fp8 GEMM with 128 x 128 block weight scales keeps its running
-# sum in units of the current group's scale product and needs both scales positive and finite.
+# Scale tensors known to be positive and finite (or not), by tensor identity and in-place version:
+# {id: (weakref, version, ok)}.  The fp8 GEMM with 128 x 128 block weight scales keeps its running sum in units
+# of the current group's scale product, which needs every activation and weight scale positive and finite.
+# Dispatch only looks the verdict up: it never reads a scale tensor, so it never waits for the device and
+# can be captured into a graph.  Scales with no verdict take the per-group fold on scales repeated per
+# channel, which is exact for any values.
 _SCALES_CHECKED = {}
 
 
@@ -34,14 +37,17 @@ def _remember_scales(t, ok):
     _SCALES_CHECKED[key] = (weakref.ref(t, lambda _r, key=key: _SCALES_CHECKED.pop(key, None)), t._version, ok)
 
 
-def _scales_positive_finite(t):
-    """True if every value of `t` is > 0 and finite: checked on the device once per tensor and version."""
+def _verdict(t):
+    """The recorded verdict for `t` as it is now: True, False, or None if there is none (no device access)."""
     hit = _SCALES_CHECKED.get(id(t))
     if hit is not None and hit[0]() is t and hit[1] == t._version:
         return hit[2]
-    ok = bool(torch.all((t > 0) & torch.isfinite(t)))
-    _remember_scales(t, ok)
-    return ok
+    return None
+
+
+def _known_positive_finite(t):
+    """True if `t`, as it is now, is recorded as positive and finite (no device access)."""
+    return _verdict(t) is True
 
 
 def trust_scales(*tensors):
@@ -50,6 +56,23 @@ def trust_scales(*tensors):
     for t in tensors:
         if t is not None:
             _remember_scales(t, True)
+
+
+def validate_scales(*tensors):
+    """Check scale tensors from elsewhere (a checkpoint's fp8 block scales) once and remember the verdict, so
+    that block_gemm / block_linear read fp8 block scales as stored.  Meant for load time: on a device tensor
+    the check waits for the device, once per tensor and in-place version; on a host tensor it does not touch
+    the device.  Returns True if every value of every tensor is positive and finite."""
+    ok_all = True
+    for t in tensors:
+        if t is None:
+            continue
+        ok = _verdict(t)
+        if ok is None:
+            ok = bool(torch.all((t > 0) & torch.isfinite(t)))
+            _remember_scales(t, ok)
+        ok_all = ok_all and ok
+    return ok_all
 
 
 def _aligned(t, bytes_):
@@ -124,19 +147,23 @@ def _layout(sw, n, k, kind, sa_cols, sa=None, swiglu=False):
 
     sw_rows = 128: one weight-scale row per 128 output channels (the fp8 block layout), read as stored by
     the per-group fold.  With fp8 codes that fold keeps its running sum in units of the current group's
-    scale product, which needs every activation and weight scale positive and finite; other scales are
-    repeated per channel instead (the reference's own layout, pixelumm.py:153), whose fold has no such
-    condition.  group = K: one scale per token and per channel, accumulated over the whole K (int8 only
-    while the int32 sum cannot overflow)."""
+    scale product, which needs every activation and weight scale positive and finite: scales made by this
+    package's quantizers, or passed through `validate_scales`.  Other scales are repeated per channel
+    instead (the reference's own layout, pixelumm.py:153), whose fold has no such condition.  The swiglu
+    epilogue has no such fallback: it checks unknown scales once (`validate_scales`).  group = K: one scale
+    per token and per channel, accumulated over the whole K (int8 only while the int32 sum cannot
+    overflow)."""
     sw_rows = 1 if sw.shape[0] == n else GROUP
     if sw_rows == GROUP and sw.shape[0] != (n + GROUP - 1) // GROUP:
         raise RuntimeError(f"weight scales with {sw.shape[0]} rows for {n} output channels")
-    if sw_rows == GROUP and kind == "fp8" and not ((sa is None or _scales_positive_finite(sa))
-                                                   and _scales_positive_finite(sw)):
+    if sw_rows == GROUP and kind == "fp8":
         if swiglu:
-            raise RuntimeError("swiglu_quant: fp8 block scales must be positive and finite")
-        sw = sw.float().repeat_interleave(GROUP, dim=0)[:n]
-        sw_rows = 1
+            if not validate_scales(*(t for t in (sa, sw) if t is not None)):
+                raise RuntimeError("swiglu_quant: fp8 block scales must be positive and finite")
+        elif not ((sa is None or _known_positive_finite(sa)) and _known_positive_finite(sw)):
+            # each block row repeated for its 128 channels (expand + copy: no device synchronization)
+            sw = sw.float()[:, None, :].expand(-1, GROUP, -1).reshape(-1, sw.shape[1])[:n]
+            sw_rows = 1
     if sw_rows == 1 and sa_cols == 1 and sw.shape[1] == 1 and (kind == "fp8" or k < WHOLE_K_INT32_LIMIT):
         return sw, sw_rows, k, 1
     return sw, sw_rows, GROUP, k // GROUP
@@ -316,12 +343,13 @@ def adaln_quant(x, shift, scale, eps=1e-6, norm="layer", rounding="half_away", g
     return q, s
 
 
-def block_linear(x, qw, sw, bias=None, kind="int8"):
+def block_linear(x, qw, sw, bias=None, kind="int8", rounding="half_away"):
     """F.linear with block-scaled 8-bit weights: x [..., K] -> [..., N] in x's dtype
     (hy_nomas/kernels.py:210-222).  Weight scales [N, K/128] select per-token-and-group activation
     quantization; per-channel scales [N, 1] select per-token quantization; block scales
     [ceil(N/128), K/128] (one row per 128 output channels) are taken as they are.  One library call
-    (hn_block_linear) quantizes into a workspace and runs the GEMM."""
+    (hn_block_linear) quantizes into a workspace and runs the GEMM.  `rounding` (an addition to the
+    reference's signature): "half_even" rounds the int8 activation codes half to even."""
     shape = x.shape
     x2 = x.reshape(-1, shape[-1])
     if not x2.is_contiguous():
@@ -341,7 +369,7 @@ def block_linear(x, qw, sw, bias=None, kind="int8"):
     if gemm_group != group:
         # per-token scales over a K the int32 sum cannot hold: quantize per token, fold per group
         with torch.cuda.device(x.device):
-            qa, sa = quantize_activations(x2, kind, None)
+            qa, sa = quantize_activations(x2, kind, None, rounding)
             out = block_gemm(qa, sa, qw, sw, bias, x.dtype, kind)
         return out.reshape(*shape[:-1], n)
     if x2.dtype not in _lib.DTYPE:
@@ -356,7 +384,7 @@ def block_linear(x, qw, sw, bias=None, kind="int8"):
     ws = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
     with torch.cuda.device(x.device):
         _lib.call("hn_block_linear", x2.data_ptr(), _lib.dtype_code(x2), x2.stride(0), m, k, group, _lib.KIND[kind],
-                  _lib.ROUND["half_away"], qw.data_ptr(), qw.stride(0), sw.data_ptr(), sw.stride(0), sw_rows,
+                  _lib.ROUND[rounding], qw.data_ptr(), qw.stride(0), sw.data_ptr(), sw.stride(0), sw_rows,
                   _lib.ptr(bias), _lib.dtype_code(bias) if bias is not None else 0, n, out.data_ptr(),
                   _lib.dtype_code(out), out.stride(0), ws.data_ptr(), nbytes, _lib.stream(x2))
     return out.reshape(*shape[:-1], n).to(x.dtype)

@@ -3,6 +3,14 @@ runs them on the gfx950 fp8 matrix cores, the decoder's SwiGLU MLP with its gate
 GEMM, and the checkpoint reader (the FP8 layout, dispatch, MLP and loader of the reference's
 `hy_nomas/pixelumm.py:35-158, 314-323, 470-485`; the rest of the decoder model is not part of this
 package).
+
+With ComfyUI importable, `DecoderOps` extends `comfy.ops.manual_cast` as the reference's does, and its fp8
+weights are `QuantizedTensor`s of the registered `NomasFP8Block128Layout` (when comfy-kitchen is present).
+Without it, `DecoderOps` is a plain torch module family with the same interface.  Either way the fp8 matmul
+reads the [N/128, K/128] block scales as stored; the reference expands them per output channel
+(`scale.repeat_interleave(128, 0)`, pixelumm.py:153), which makes the GEMM fold every channel's scale
+separately.  Block scales are checked once, when a Linear loads them (positive and finite, on the host
+tensor), and the per-call device copies inherit that verdict, so no forward waits for the device.
 """
 import dataclasses
 
@@ -10,6 +18,20 @@ import torch
 import torch.nn.functional as F
 
 from . import kernels
+
+try:
+    import comfy.model_management  # noqa: F401
+    import comfy.ops
+    from comfy.quant_ops import QuantizedTensor
+    _COMFY = True
+except ImportError:
+    _COMFY = False
+
+try:
+    from comfy_kitchen.tensor import BaseLayoutParams, QuantizedLayout, register_layout_class
+    _CK = True
+except ImportError:
+    _CK = False
 
 FP8_FORMAT = "pixelumm_fp8_bf16_single_v1"
 FP8_LAYOUT = "NomasFP8Block128Layout"
@@ -59,54 +81,181 @@ def fp8_block_linear(x, qdata, scale, bias=None):
     return kernels.block_linear(x, qdata, scale, bias, kind="fp8")
 
 
-class DecoderOps:
-    """Linear with `fp8_weight` / `fp8_scale` pairs.  `matmul`: "dequant" runs bf16 GEMMs on dequantized
-    weights, "fp8" runs the fp8 matrix-core GEMM."""
+if _CK:
+    class NomasFP8Block128Layout(QuantizedLayout):
+        """The decoder's FP8 weights as a comfy-kitchen layout (hy_nomas/pixelumm.py:65-96): e4m3fn codes with
+        one fp32 scale per 128 x 128 block, saved as `<name>.fp8_weight` / `<name>.fp8_scale`."""
+        MIN_SM_VERSION = None
 
-    @classmethod
-    def with_matmul(cls, matmul):
-        linear = type("Linear", (cls.Linear,), {"matmul": matmul})
-        return type(f"DecoderOps_{matmul}", (cls,), {"Linear": linear})
+        @dataclasses.dataclass(frozen=True)
+        class Params(BaseLayoutParams):
+            pass
 
-    class Linear(torch.nn.Module):
-        matmul = "dequant"
+        @classmethod
+        def quantize(cls, tensor, scale=None, **kwargs):
+            q, s = quantize_fp8_block(tensor)
+            return q, cls.Params(scale=s, orig_dtype=tensor.dtype, orig_shape=tuple(tensor.shape))
 
-        def __init__(self, in_features, out_features, bias=True, device=None, dtype=None):
-            super().__init__()
-            self.in_features, self.out_features = in_features, out_features
-            self.weight = None
-            self.scale = None
-            self.bias = None
-            self._has_bias = bias
-            self._dtype = dtype
+        @classmethod
+        def dequantize(cls, qdata, params):
+            return dequantize_fp8_block(qdata, params.scale, params.orig_dtype)
 
-        def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
-                                  unexpected_keys, error_msgs):
-            q = state_dict.pop(prefix + "fp8_weight", None)
-            s = state_dict.pop(prefix + "fp8_scale", None)
-            w = state_dict.pop(prefix + "weight", None)
-            b = state_dict.pop(prefix + "bias", None)
-            if q is not None:
-                self.weight, self.scale = q, s.float()
-            elif w is not None:
-                self.weight = w.to(self._dtype) if self._dtype is not None else w
-            else:
-                missing_keys.append(prefix + "weight")
-                return
-            if b is not None:
-                self.bias = b.to(self._dtype) if self._dtype is not None else b
-            elif self._has_bias:
-                missing_keys.append(prefix + "bias")
+        @classmethod
+        def get_plain_tensors(cls, qtensor):
+            return qtensor._qdata, qtensor._params.scale
 
-        def forward(self, input):
-            weight = self.weight.to(input.device)
-            bias = self.bias.to(device=input.device, dtype=input.dtype) if self.bias is not None else None
-            if self.scale is not None:
-                scale = self.scale.to(input.device)
-                if self.matmul == "fp8" and input.is_cuda:
-                    return fp8_block_linear(input, weight, scale, bias)
-                weight = dequantize_fp8_block(weight, scale, input.dtype)
-            return F.linear(input, weight.to(input.dtype), bias)
+        @classmethod
+        def state_dict_tensors(cls, qdata, params):
+            return {".fp8_weight": qdata, ".fp8_scale": params.scale}
+
+    register_layout_class(FP8_LAYOUT, NomasFP8Block128Layout)
+else:
+    NomasFP8Block128Layout = None
+
+
+def _scales_ok(lin, scale):
+    """Whether the linear's stored block scales are positive and finite: decided once per stored tensor and
+    in-place version (`kernels.validate_scales`; at load time the tensor is the checkpoint's host copy, so the
+    check does not touch the device)."""
+    if lin._scale_src is not scale or lin._scale_version != scale._version:
+        lin._scale_ok = kernels.validate_scales(scale)
+        lin._scale_src, lin._scale_version = scale, scale._version
+    return lin._scale_ok
+
+
+def _load_fp8_pair(lin, state_dict, prefix, missing_keys):
+    """(codes, fp32 block scales, plain weight, bias) from `fp8_weight` / `fp8_scale` or `weight`, and `bias`
+    (hy_nomas/pixelumm.py:128-143); the plain weight and the bias in the layer dtype.  None for a missing
+    weight (reported in `missing_keys`)."""
+    q = state_dict.pop(prefix + "fp8_weight", None)
+    s = state_dict.pop(prefix + "fp8_scale", None)
+    w = state_dict.pop(prefix + "weight", None)
+    b = state_dict.pop(prefix + "bias", None)
+    if q is None and w is None:
+        missing_keys.append(prefix + "weight")
+        return None
+    if q is not None:
+        s = s.float()
+        _scales_ok(lin, s)
+        w = None
+    elif lin._dtype is not None:
+        w = w.to(lin._dtype)
+    if b is not None:
+        b = b.to(lin._dtype) if lin._dtype is not None else b
+    elif lin._has_bias:
+        missing_keys.append(prefix + "bias")
+    return q, s, w, b
+
+
+def _fp8_forward(lin, input, qdata, scale, stored_scale, bias):
+    """F.linear on fp8 block weights: the fp8 matrix-core GEMM with the block scales as stored (a device
+    copy of checked scales inherits their verdict), or dequantize + F.linear (pixelumm.py:147-155)."""
+    if lin.matmul == "fp8" and input.is_cuda:
+        if _scales_ok(lin, stored_scale):
+            kernels.trust_scales(scale)
+        return fp8_block_linear(input, qdata, scale, bias)
+    return F.linear(input, dequantize_fp8_block(qdata, scale, input.dtype), bias)
+
+
+def _init_linear(lin, in_features, out_features, bias, dtype):
+    lin.in_features, lin.out_features = in_features, out_features
+    lin.weight = None
+    lin.bias = None
+    lin._has_bias = bias
+    lin._dtype = dtype
+    lin._scale_src, lin._scale_version, lin._scale_ok = None, None, False
+
+
+if _COMFY:
+    class DecoderOps(comfy.ops.manual_cast):
+        """ComfyUI's cast-on-use ops with a Linear that also loads `fp8_weight` / `fp8_scale` pairs into
+        `QuantizedTensor`s of the FP8 block-128 layout.  `matmul`: "dequant" runs bf16 GEMMs on dequantized
+        weights, "fp8" the fp8 matrix-core GEMM (activations quantized per token and 128 channels)."""
+
+        @classmethod
+        def with_matmul(cls, matmul):
+            linear = type("Linear", (cls.Linear,), {"matmul": matmul})
+            return type(f"DecoderOps_{matmul}", (cls,), {"Linear": linear})
+
+        class Linear(comfy.ops.manual_cast.Linear):
+            matmul = "dequant"
+
+            def __init__(self, in_features, out_features, bias=True, device=None, dtype=None):
+                torch.nn.Module.__init__(self)
+                _init_linear(self, in_features, out_features, bias, dtype)
+
+            def reset_parameters(self):
+                return None
+
+            def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs):
+                got = _load_fp8_pair(self, state_dict, prefix, missing_keys)
+                if got is None:
+                    return
+                q, s, w, b = got
+                if q is not None:
+                    if NomasFP8Block128Layout is None:
+                        raise RuntimeError("PixelUMM FP8 weights need comfy-kitchen (it ships with ComfyUI)")
+                    params = NomasFP8Block128Layout.Params(scale=s, orig_dtype=self._dtype or torch.bfloat16,
+                                                           orig_shape=tuple(q.shape))
+                    w = QuantizedTensor(q, FP8_LAYOUT, params)
+                self.weight = torch.nn.Parameter(w, requires_grad=False)
+                if b is not None:
+                    self.bias = torch.nn.Parameter(b, requires_grad=False)
+
+            def forward_comfy_cast_weights(self, input):
+                with comfy.ops.CastBiasWeightContext(self, input, offloadable=True) as (weight, bias):
+                    if isinstance(weight, QuantizedTensor):
+                        return _fp8_forward(self, input, weight._qdata, weight._params.scale,
+                                            self.weight._params.scale, bias)
+                    return F.linear(input, weight, bias)
+
+            def forward(self, *args, **kwargs):
+                return self.forward_comfy_cast_weights(*args, **kwargs)
+
+            def fp8_parts(self):
+                """(codes, block scales) as stored, or None for a plain weight."""
+                if isinstance(self.weight, QuantizedTensor):
+                    return self.weight._qdata, self.weight._params.scale
+                return None
+else:
+    class DecoderOps:
+        """Linear with `fp8_weight` / `fp8_scale` pairs.  `matmul`: "dequant" runs bf16 GEMMs on dequantized
+        weights, "fp8" runs the fp8 matrix-core GEMM."""
+
+        @classmethod
+        def with_matmul(cls, matmul):
+            linear = type("Linear", (cls.Linear,), {"matmul": matmul})
+            return type(f"DecoderOps_{matmul}", (cls,), {"Linear": linear})
+
+        class Linear(torch.nn.Module):
+            matmul = "dequant"
+
+            def __init__(self, in_features, out_features, bias=True, device=None, dtype=None):
+                super().__init__()
+                _init_linear(self, in_features, out_features, bias, dtype)
+                self.scale = None
+
+            def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs):
+                got = _load_fp8_pair(self, state_dict, prefix, missing_keys)
+                if got is None:
+                    return
+                q, s, w, b = got
+                self.weight, self.scale = (q, s) if q is not None else (w, None)
+                if b is not None:
+                    self.bias = b
+
+            def forward(self, input):
+                weight = self.weight.to(input.device)
+                bias = self.bias.to(device=input.device, dtype=input.dtype) if self.bias is not None else None
+                if self.scale is not None:
+                    return _fp8_forward(self, input, weight, self.scale.to(input.device), self.scale, bias)
+                return F.linear(input, weight.to(input.dtype), bias)
+
+            def fp8_parts(self):
+                """(codes, block scales) as stored, or None for a plain weight."""
+                return (self.weight, self.scale) if self.scale is not None else None
 
 
 def interleave_gate_up(gate, up):
@@ -122,6 +271,8 @@ def interleave_gate_up(gate, up):
     q = torch.stack((as_bytes(qg).reshape(i // 128, 128, k), as_bytes(qu).reshape(i // 128, 128, k)), dim=1)
     q = q.reshape(2 * i, k).view(qg.dtype)
     s = torch.stack((sg.float(), su.float()), dim=1).reshape(2 * i // 128, sg.shape[1]).contiguous()
+    if kernels._known_positive_finite(sg) and kernels._known_positive_finite(su):
+        kernels.trust_scales(s)  # the same values, rearranged
     return q, s
 
 
@@ -146,8 +297,9 @@ def swiglu_mlp(x, gate_up, down, bias=None):
 
 class MLP(torch.nn.Module):
     """The decoder MLP (hy_nomas/pixelumm.py:314-323) over `ops.Linear`s.  With fp8 weights on all three
-    projections, `matmul == "fp8"` and a device input, the forward is `swiglu_mlp` (gate and up in one
-    GEMM); otherwise it is the reference's expression."""
+    projections, `matmul == "fp8"`, scales that passed the load-time check, no ComfyUI weight or bias patches
+    (LoRA hooks) and a device input, the forward is `swiglu_mlp` (gate and up in one GEMM); otherwise it is
+    the reference's expression."""
 
     def __init__(self, arch, ops, dtype=None, device=None):
         super().__init__()
@@ -157,20 +309,27 @@ class MLP(torch.nn.Module):
         self.down_proj = ops.Linear(arch.intermediate_size, arch.hidden_size, bias=False, **kw)
         self._fused = None
 
-    def _fused_weights(self, device):
-        key = (device, self.gate_proj.weight.data_ptr(), self.up_proj.weight.data_ptr())
+    @staticmethod
+    def _fusable(lin):
+        parts = lin.fp8_parts() if getattr(lin, "matmul", None) == "fp8" and hasattr(lin, "fp8_parts") else None
+        if parts is None or getattr(lin, "weight_function", None) or getattr(lin, "bias_function", None):
+            return None
+        return parts if _scales_ok(lin, parts[1]) else None
+
+    def _fused_weights(self, device, gate, up):
+        key = (device, gate[0].data_ptr(), up[0].data_ptr(), gate[1]._version, up[1]._version)
         if self._fused is None or self._fused[0] != key:
-            gate = (self.gate_proj.weight.to(device), self.gate_proj.scale.to(device))
-            up = (self.up_proj.weight.to(device), self.up_proj.scale.to(device))
-            self._fused = (key, interleave_gate_up(gate, up))
+            q, s = interleave_gate_up((gate[0].to(device), gate[1].to(device)), (up[0].to(device), up[1].to(device)))
+            kernels.trust_scales(s)  # both sources passed the check
+            self._fused = (key, (q, s))
         return self._fused[1]
 
     def forward(self, x):
-        lins = (self.gate_proj, self.up_proj, self.down_proj)
-        if (x.is_cuda and all(getattr(l, "matmul", None) == "fp8" and getattr(l, "scale", None) is not None
-                              for l in lins)):
-            down = (self.down_proj.weight.to(x.device), self.down_proj.scale.to(x.device))
-            return swiglu_mlp(x, self._fused_weights(x.device), down)
+        parts = [self._fusable(l) for l in (self.gate_proj, self.up_proj, self.down_proj)]
+        if x.is_cuda and all(p is not None for p in parts):
+            down = (parts[2][0].to(x.device), parts[2][1].to(x.device))
+            kernels.trust_scales(down[1])
+            return swiglu_mlp(x, self._fused_weights(x.device, parts[0], parts[1]), down)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 

@@ -265,9 +265,11 @@ def test_block_weight_scales(dev, kind, m, n, k):
     qa_t = torch.from_numpy(qa)
     if kind == "fp8":
         qa_t = qa_t.view(torch.float8_e4m3fn)
-    args = (qa_t.to(dev), torch.from_numpy(sa).to(dev), codes.to(dev))
+    sa_t, sblk_t = torch.from_numpy(sa).to(dev), sblk.to(dev)
+    assert kernels.validate_scales(sa_t, sblk_t)  # fp8: the block scales are read as stored
+    args = (qa_t.to(dev), sa_t, codes.to(dev))
     # fp32 outputs, so that the fold's rounding is not hidden behind (or magnified by) a bf16 rounding
-    got = kernels.block_gemm(*args, sblk.to(dev), bias.to(dev), torch.float32, kind=kind).cpu().numpy()
+    got = kernels.block_gemm(*args, sblk_t, bias.to(dev), torch.float32, kind=kind).cpu().numpy()
     full = kernels.block_gemm(*args, sw_full.to(dev), bias.to(dev), torch.float32, kind=kind).cpu().numpy()
     exact = fp64_dequant_product(qa, sa, w_codes, sw_full.numpy(), bias, kind=kind)
     assert max_abs_rel(got, exact) < 1e-2
@@ -325,8 +327,12 @@ def test_fp8_block_linear(dev):
     x = (torch.randn(3, 170, 1024, generator=g) * 0.5).to(torch.bfloat16)
     w = torch.randn(768, 1024, generator=g) * 0.02
     bias = (torch.randn(768, generator=g) * 0.02).to(torch.bfloat16)
+    from hy_nomas import kernels
+
     qw, sblk = pixelumm.quantize_fp8_block(w)
-    got = pixelumm.fp8_block_linear(x.to(dev), qw.to(dev), sblk.to(dev), bias.to(dev)).cpu().float()
+    sblk_dev = sblk.to(dev)
+    assert kernels.validate_scales(sblk_dev)
+    got = pixelumm.fp8_block_linear(x.to(dev), qw.to(dev), sblk_dev, bias.to(dev)).cpu().float()
     ref = torch.nn.functional.linear(x.float(), pixelumm.dequantize_fp8_block(qw, sblk, torch.float32),
                                      bias.float())
     assert got.shape == (3, 170, 768)
@@ -446,3 +452,114 @@ def test_config0_half_even_chain(dev):
     assert torch.equal(out.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
     exact = fp64_dequant_product(q_ref, s_ref, w.numpy(), sw.numpy(), bias)
     assert max_abs_rel(out.cpu().float().numpy(), exact) < 1e-2
+
+
+@pytest.mark.parametrize("m,k,n,layout", [
+    (1000, 3072, 1536, "g128"), (300, 1024, 640, "g128"), (77, 256, 384, "g128"),
+    (1000, 3072, 1536, "per_token"), (513, 12288, 256, "per_token"), (5, 2048, 768, "per_token")])
+def test_block_linear_equals_the_oracle_chain(dev, m, k, n, layout):
+    """kernels.block_linear (one hn_block_linear call: activation quantization into a workspace, then the GEMM)
+    against the oracle's quantize + block_gemm on the same bf16 input, bit for bit: g128 weights with
+    per-token-and-group codes, per-channel weights with per-token codes (hy_nomas/kernels.py:210-222)."""
+    from hy_nomas import kernels
+
+    print(f"block_linear vs oracle chain {layout} m={m} k={k} n={n}", flush=True)
+    x = outlier_input(m, k, seed=m + k + n)
+    w, sw, bias = int8_weights(n, k, seed=n + 5 * k, per_channel=layout == "per_token")
+    got = kernels.block_linear(x.view(1, m, k).to(dev), w.to(dev), sw.to(dev), bias.to(dev)).cpu()
+    assert got.shape == (1, m, n) and got.dtype == torch.bfloat16
+    qa, sa = oracle.quantize(x, 128 if layout == "g128" else k)
+    ref = oracle.block_gemm(qa, sa, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    want = torch.from_numpy(ref).to(torch.bfloat16)
+    diff = (got[0].view(torch.int16) != want.view(torch.int16)).nonzero()
+    assert diff.numel() == 0, f"{len(diff)} outputs differ from the oracle chain, first {diff[:3].tolist()}"
+
+
+def test_block_linear_config0_half_even_equals_the_oracle_chain(dev):
+    """Config 0 (x bf16 [1024, 3072] with 1 % outlier channels x20, per-channel int8 weights [3072, 3072], bf16
+    bias) through the one-call linear with round-half-even per-token codes: bit-identical to the oracle's
+    half-even quantization + GEMM, and within 1e-2 of the fp64 product of the dequantized operands."""
+    from hy_nomas import kernels
+
+    print("block_linear config 0 half-even", flush=True)
+    m, k, n = 1024, 3072, 3072
+    g = seeded(0)
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[: k // 100]] *= 20
+    x = x.to(torch.bfloat16)
+    w, sw, bias = int8_weights(n, k, seed=1, per_channel=True)
+    got = kernels.block_linear(x.to(dev), w.to(dev), sw.to(dev), bias.to(dev), rounding="half_even").cpu()
+    q_ref, s_ref = oracle.quantize(x, k, "int8", rounding="half_even")
+    ref = oracle.block_gemm(q_ref, s_ref, w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    assert torch.equal(got, torch.from_numpy(ref).to(torch.bfloat16))
+    away = kernels.block_linear(x.to(dev), w.to(dev), sw.to(dev), bias.to(dev)).cpu()
+    assert not torch.equal(away, got)  # ties occur at this size: the rounding mode reached the quantizer
+    assert max_abs_rel(got.float().numpy(), fp64_dequant_product(q_ref, s_ref, w.numpy(), sw.numpy(), bias)) < 1e-2
+
+
+@pytest.mark.parametrize("m,k,n", [(1000, 3072, 1536), (300, 1024, 640), (64, 12288, 384)])
+def test_fp8_block_linear_equals_the_oracle_chain(dev, m, k, n):
+    """pixelumm.fp8_block_linear (one hn_block_linear call, e4m3 codes per token and 128 channels, block weight
+    scales read as stored) against the oracle's fp8 quantize + block_gemm on the scales repeated per channel:
+    the codes and scales are the oracle's, so only the fp32 accumulation order differs (< 4e-3); and the same
+    call on scales without a recorded verdict (the per-channel fold) agrees likewise."""
+    from hy_nomas import kernels, pixelumm
+
+    print(f"fp8 block_linear vs oracle chain m={m} k={k} n={n}", flush=True)
+    g = seeded(m * 3 + k + n)
+    x = outlier_input(m, k, seed=m + 17)
+    qw, sblk = pixelumm.quantize_fp8_block(torch.randn(n, k, generator=g) * 0.02)
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    sblk_dev = sblk.to(dev)
+    assert kernels.validate_scales(sblk_dev)
+    # the bf16 values as fp32: the same codes and scales (exact division), and fp32 outputs, so the comparison
+    # is not blurred by a bf16 rounding of the result
+    xf = x.float().to(dev)
+    got = pixelumm.fp8_block_linear(xf, qw.to(dev), sblk_dev, bias.to(dev)).cpu().numpy()
+    assert got.dtype == np.float32
+    qa, sa = oracle.quantize(x, 128, "fp8")
+    sw_full = sblk.repeat_interleave(128, 0)[:n].contiguous().numpy()
+    ref = oracle.block_gemm(qa, sa, qw.view(torch.uint8).numpy(), sw_full, oracle.to_f32(bias), kind="fp8")
+    assert max_abs_rel(got, ref) < 4e-3
+    exact = fp64_dequant_product(qa, sa, qw.view(torch.uint8).numpy(), sw_full, bias, kind="fp8")
+    assert max_abs_rel(got, exact) < 1e-2
+    unverified = pixelumm.fp8_block_linear(xf, qw.to(dev), sblk.to(dev), bias.to(dev)).cpu().numpy()
+    assert max_abs_rel(unverified, ref) < 4e-3
+    # and the bf16 input's own call: its output rounded once to bf16
+    got16 = pixelumm.fp8_block_linear(x.to(dev), qw.to(dev), sblk_dev, bias.to(dev)).cpu()
+    assert torch.equal(got16, torch.from_numpy(got).to(torch.bfloat16))
+
+
+def test_fp8_block_dispatch_does_not_synchronize(dev):
+    """With fp8 128 x 128 block weight scales, choosing the GEMM's scale layout never waits for the device:
+    scales without a recorded verdict (a fresh device copy, an activation-scale copy) go to the per-channel
+    fold, which is bit-identical to passing the scales repeated per channel; scales that passed
+    `validate_scales` once are read as stored."""
+    from hy_nomas import kernels, pixelumm
+
+    print("fp8 block dispatch without synchronization", flush=True)
+    g = seeded(515)
+    m, k, n = 700, 1024, 640
+    x = outlier_input(m, k, seed=516).to(dev)
+    qa, sa = kernels.quantize_activations(x, "fp8")
+    qw, sblk = pixelumm.quantize_fp8_block(torch.randn(n, k, generator=g) * 0.02)
+    qw, sblk_dev, bias = qw.to(dev), sblk.to(dev), (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    sa_copy = sa.clone()
+    sw_known = sblk_dev.clone()
+    kernels.trust_scales(sw_known)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        fresh_sw = kernels.block_gemm(qa, sa, qw, sblk_dev, bias, torch.float32, kind="fp8")
+        fresh_sa = kernels.block_gemm(qa, sa_copy, qw, sw_known, bias, torch.float32, kind="fp8")
+        linear = kernels.block_linear(x, qw, sblk_dev, bias, kind="fp8")
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    expanded = sblk_dev.repeat_interleave(128, 0)[:n].contiguous()
+    want = kernels.block_gemm(qa, sa, qw, expanded, bias, torch.float32, kind="fp8")
+    assert torch.equal(fresh_sw, want) and torch.equal(fresh_sa, want)
+    assert torch.equal(linear, kernels.block_linear(x, qw, expanded, bias, kind="fp8"))
+    assert kernels.validate_scales(sblk_dev)
+    stored = kernels.block_gemm(qa, sa, qw, sblk_dev, bias, torch.float32, kind="fp8")
+    assert not torch.equal(stored, want)  # the rescaled running sum rounds differently...
+    assert max_abs_rel(stored.cpu().numpy(), want.cpu().numpy()) < 4e-3  # ...within the fp8 tolerance

@@ -296,3 +296,37 @@ def test_attention_reference_signature_and_segments_cpu():
         for plan in (NoGroups(), Plan()):
             assert torch.allclose(torch_forms.segment_attention(q, k, v, hist, plan.groups, lv),
                                   attention.segment_attention(q, k, v, hist, plan, {}), atol=1e-5)
+
+
+def test_fp8_block_scale_dispatch_reads_only_recorded_verdicts():
+    """fp8 with 128 x 128 block weight scales: the GEMM reads them as stored only when the activation and weight
+    scales are recorded as positive and finite (this package's quantizers, or `validate_scales`); otherwise the
+    block rows are repeated per channel, the layout whose fold takes any values.  Deciding never reads a scale
+    tensor, and an in-place change drops the verdict."""
+    from hy_nomas import kernels
+
+    n, k = 300, 512
+    g = torch.Generator().manual_seed(40)
+    s = torch.rand(3, 4, generator=g) + 0.1
+    sw, rows, group, groups = kernels._layout(s, n, k, "fp8", 4)
+    assert rows == 1 and group == 128 and groups == 4 and sw.shape == (n, 4)
+    assert torch.equal(sw, s.repeat_interleave(128, 0)[:n])
+    assert kernels.validate_scales(s)
+    sw, rows, _, _ = kernels._layout(s, n, k, "fp8", 4)
+    assert rows == 128 and sw is s
+    s[0, 0] = 0.0                      # in place: the verdict no longer applies
+    assert kernels._layout(s, n, k, "fp8", 4)[1] == 1
+    assert not kernels.validate_scales(s)
+    assert kernels._layout(s, n, k, "fp8", 4)[1] == 1
+    for bad in (float("inf"), float("nan"), -1e-3):
+        t = torch.rand(3, 4, generator=g) + 0.1
+        t[2, 3] = bad
+        assert not kernels.validate_scales(t) and kernels._layout(t, n, k, "fp8", 4)[1] == 1
+    # activation scales from elsewhere need a verdict too
+    sw_ok = torch.rand(3, 4, generator=g) + 0.1
+    kernels.trust_scales(sw_ok)
+    sa = torch.rand(8, 4, generator=g) + 0.1
+    assert kernels._layout(sw_ok, n, k, "fp8", 4, sa)[1] == 1
+    assert kernels.validate_scales(sa) and kernels._layout(sw_ok, n, k, "fp8", 4, sa)[1] == 128
+    # int8 block scales fold without a ratio: no verdict needed
+    assert kernels._layout(torch.rand(3, 4, generator=g), n, k, "int8", 4)[1] == 128

@@ -7,10 +7,11 @@ module uses:
   dequantizes through its registered layout;
 - `comfy_kitchen.tensor`: `BaseLayoutParams`, `QuantizedLayout`, `register_layout_class`.
 
-It then loads a fresh `hy_nomas.ops` against them and runs the subclass on the CPU.  The stand-in is test
-infrastructure: it pins the logic of the ComfyUI branch (state-dict loading into the registered layout, the
-cast context, exact forward, weight conversion and re-quantization, the matmul variants), not ComfyUI's own
-behaviour."""
+It then loads a fresh `hy_nomas.ops` (and `hy_nomas.pixelumm`, the decoder's FP8 ops) against them and runs
+the subclasses on the CPU, and the decoder's fp8 matmul on the GPU.  The stand-in is test infrastructure: it
+pins the logic of the ComfyUI branches (state-dict loading into the registered layouts, the cast context,
+exact and dequantized forwards, weight conversion and re-quantization, the matmul variants, the block scales
+handed to the fp8 GEMM as stored), not ComfyUI's own behaviour."""
 import dataclasses
 import importlib
 import sys
@@ -69,9 +70,13 @@ class CastBiasWeightContext:
     def __enter__(self):
         CASTS.append(type(self.module).__name__)
         w, b = self.module.weight, self.module.bias
+        dev = self.input.device
         if not isinstance(w, QuantizedTensor):
-            w = w.to(self.input.dtype)
-        return w, (b.to(self.input.dtype) if b is not None else None)
+            w = w.to(device=dev, dtype=self.input.dtype)
+        elif w._qdata.device != dev:  # a quantized weight moves as codes + layout parameters
+            params = dataclasses.replace(w._params, scale=w._params.scale.to(dev))
+            w = QuantizedTensor(w._qdata.to(dev), w._layout, params)
+        return w, (b.to(device=dev, dtype=self.input.dtype) if b is not None else None)
 
     def __exit__(self, *exc):
         return False
@@ -84,8 +89,7 @@ class _ManualCast:
         bias_function = []
 
 
-@pytest.fixture
-def comfy_ops(monkeypatch):
+def _install_comfy(monkeypatch):
     comfy = types.ModuleType("comfy")
     mm = types.ModuleType("comfy.model_management")
     cops = types.ModuleType("comfy.ops")
@@ -102,22 +106,38 @@ def comfy_ops(monkeypatch):
     for name, mod in (("comfy", comfy), ("comfy.model_management", mm), ("comfy.ops", cops),
                       ("comfy.quant_ops", qops), ("comfy_kitchen", ck), ("comfy_kitchen.tensor", ckt)):
         monkeypatch.setitem(sys.modules, name, mod)
-    saved = sys.modules.pop("hy_nomas.ops", None)
+
+
+def _fresh_module(monkeypatch, name):
+    """A fresh import of hy_nomas.<name> against the stand-in (the package's own module is restored after)."""
+    _install_comfy(monkeypatch)
+    full = f"hy_nomas.{name}"
+    saved = sys.modules.pop(full, None)
     import hy_nomas
-    saved_attr = getattr(hy_nomas, "ops", None)
+    saved_attr = getattr(hy_nomas, name, None)
     try:
-        ops = importlib.import_module("hy_nomas.ops")
-        assert ops._COMFY and ops._CK
+        mod = importlib.import_module(full)
+        assert mod._COMFY and mod._CK
         LAYOUTS.clear()
         CASTS.clear()
-        importlib.reload(ops)  # registers the layout with this test's registry
-        yield ops
+        importlib.reload(mod)  # registers the layout with this test's registry
+        yield mod
     finally:
-        sys.modules.pop("hy_nomas.ops", None)
+        sys.modules.pop(full, None)
         if saved is not None:
-            sys.modules["hy_nomas.ops"] = saved
+            sys.modules[full] = saved
         if saved_attr is not None:
-            hy_nomas.ops = saved_attr
+            setattr(hy_nomas, name, saved_attr)
+
+
+@pytest.fixture
+def comfy_ops(monkeypatch):
+    yield from _fresh_module(monkeypatch, "ops")
+
+
+@pytest.fixture
+def comfy_pixelumm(monkeypatch):
+    yield from _fresh_module(monkeypatch, "pixelumm")
 
 
 def _weights(n, k, seed):
@@ -207,3 +227,126 @@ def test_comfyui_linear_plain_weights_and_load_errors(comfy_ops):
     missing = []
     ops.NomasOps.Linear(k, n)._load_from_state_dict({"bias": bias}, "", {}, True, missing, [], [])
     assert missing == ["weight"]
+
+
+def _fp8_state(n, k, seed, device="cpu"):
+    """fp8_weight / fp8_scale / bias of one decoder linear, as the FP8 checkpoint holds them."""
+    from hy_nomas import pixelumm
+
+    w, bias = _weights(n, k, seed)
+    q, sblk = pixelumm.quantize_fp8_block(w)
+    return {"fp8_weight": q.to(device), "fp8_scale": sblk.clone().to(device), "bias": bias.to(device)}
+
+
+def test_comfyui_decoder_linear_loads_the_fp8_layout_and_dequantizes(comfy_pixelumm):
+    """The decoder's Linear on the ComfyUI side (hy_nomas/pixelumm.py:99-158): fp8_weight / fp8_scale load into a
+    QuantizedTensor of the registered NomasFP8Block128Layout; the dequant path (and the fp8 variant on a host
+    input) is F.linear on the dequantized weight through ComfyUI's cast context; the block scales are checked
+    on the host at load; plain weights and missing keys behave as the reference's."""
+    px = comfy_pixelumm
+    n, k = 256, 384
+    sd = _fp8_state(n, k, 11)
+    q, sblk, bias = sd["fp8_weight"], sd["fp8_scale"], sd["bias"]
+    lin = px.DecoderOps.Linear(k, n, dtype=torch.bfloat16)
+    assert isinstance(lin, torch.nn.Linear) and lin.weight is None
+    missing = []
+    lin._load_from_state_dict({"d.fp8_weight": q, "d.fp8_scale": sblk, "d.bias": bias}, "d.", {}, True, missing,
+                              [], [])
+    assert not missing
+    assert isinstance(lin.weight, QuantizedTensor) and lin.weight._layout == px.FP8_LAYOUT
+    assert LAYOUTS[px.FP8_LAYOUT] is px.NomasFP8Block128Layout
+    assert torch.equal(lin.weight._qdata.view(torch.uint8), q.view(torch.uint8))
+    assert torch.equal(lin.weight._params.scale, sblk)
+    assert lin.weight._params.scale.shape == (n // 128, k // 128)  # stored per block, not per channel
+    assert lin._scale_ok and px.kernels._known_positive_finite(lin.weight._params.scale)
+    x = torch.randn(7, k, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    CASTS.clear()
+    y = lin(x)
+    assert CASTS == ["Linear"]
+    assert torch.equal(y, F.linear(x, px.dequantize_fp8_block(q, sblk, torch.bfloat16), bias))
+    fp8 = px.DecoderOps.with_matmul("fp8").Linear(k, n, dtype=torch.bfloat16)
+    assert issubclass(px.DecoderOps.with_matmul("fp8"), px.DecoderOps) and fp8.matmul == "fp8"
+    fp8._load_from_state_dict(dict(sd), "", {}, True, [], [], [])
+    assert torch.equal(fp8(x), y)  # a host input takes the dequant path
+    # the layout class: its quantization is quantize_fp8_block, and it saves the checkpoint's key names
+    w, _ = _weights(n, k, 11)
+    qq, params = px.NomasFP8Block128Layout.quantize(w)
+    assert torch.equal(qq.view(torch.uint8), q.view(torch.uint8)) and torch.equal(params.scale, sblk)
+    assert torch.equal(px.NomasFP8Block128Layout.dequantize(qq, params), px.dequantize_fp8_block(q, sblk, w.dtype))
+    assert set(px.NomasFP8Block128Layout.state_dict_tensors(qq, params)) == {".fp8_weight", ".fp8_scale"}
+    assert px.NomasFP8Block128Layout.get_plain_tensors(lin.weight)[1] is lin.weight._params.scale
+    # a zero block scale is recorded as failing the check (the fp8 GEMM then folds scales per channel)
+    bad = dict(_fp8_state(n, k, 13))
+    bad["fp8_scale"][1, 2] = 0.0
+    lin_bad = px.DecoderOps.Linear(k, n)
+    lin_bad._load_from_state_dict(bad, "", {}, True, [], [], [])
+    assert not lin_bad._scale_ok
+    # plain weights, a missing bias, a missing weight
+    plain = px.DecoderOps.Linear(k, n, dtype=torch.bfloat16)
+    missing = []
+    plain._load_from_state_dict({"weight": w}, "", {}, True, missing, [], [])
+    assert missing == ["bias"] and plain.weight.dtype == torch.bfloat16
+    assert not isinstance(plain.weight, QuantizedTensor) and plain.fp8_parts() is None
+    assert torch.equal(plain(x), F.linear(x, w.to(torch.bfloat16)))
+    missing = []
+    px.DecoderOps.Linear(k, n)._load_from_state_dict({}, "p.", {}, True, missing, [], [])
+    assert missing == ["p.weight"]
+
+
+@pytest.mark.gpu
+def test_comfyui_decoder_fp8_path_reads_block_scales_as_stored(comfy_pixelumm, dev, monkeypatch):
+    """The fp8 matmul through the ComfyUI branch: the GEMM receives the [N/128, K/128] block scales as stored
+    (sw_rows = 128 at the C ABI; the reference passes them repeated per channel, pixelumm.py:153), the result is
+    bit-identical to pixelumm.fp8_block_linear, the per-call device copy of the host-checked scales needs no
+    device check, and weights resident on the device run without any synchronization.  The fused SwiGLU MLP
+    takes the ComfyUI weights too."""
+    px = comfy_pixelumm
+    from hy_nomas import _lib
+
+    print("ComfyUI decoder fp8 path", flush=True)
+    n, k = 512, 1024
+    calls = []
+    real_call = _lib.call
+
+    def spy(name, *args):
+        calls.append((name, args))
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", spy)
+    sd = _fp8_state(n, k, 21)
+    x = (torch.randn(3, 50, k, generator=torch.Generator().manual_seed(22)) * 2).to(torch.bfloat16).to(dev)
+    for resident in (False, True):
+        lin = px.DecoderOps.with_matmul("fp8").Linear(k, n, dtype=torch.bfloat16)
+        state = {key: v.to(dev) for key, v in sd.items()} if resident else dict(sd)
+        lin._load_from_state_dict(state, "", {}, True, [], [], [])
+        torch.cuda.synchronize()
+        calls.clear()
+        if resident:
+            torch.cuda.set_sync_debug_mode("error")
+        try:
+            y = lin(x)
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+        lin_calls = [a for name, a in calls if name == "hn_block_linear"]
+        assert len(lin_calls) == 1 and lin_calls[0][12] == 128, "block scales must reach the GEMM as stored"
+        s_ref = sd["fp8_scale"].to(dev)
+        assert px.kernels.validate_scales(s_ref)  # the same block-scale path as the module's call
+        ref = px.fp8_block_linear(x, sd["fp8_weight"].to(dev), s_ref, sd["bias"].to(dev))
+        assert torch.equal(y, ref)
+        want = F.linear(x.float(), px.dequantize_fp8_block(sd["fp8_weight"], sd["fp8_scale"], torch.float32).to(dev),
+                        sd["bias"].float().to(dev))
+        assert ((y.float() - want).abs().max() / want.abs().max()).item() < 3e-2
+    # the decoder MLP on ComfyUI weights: gate and up in one SwiGLU GEMM, then down
+    arch = px.Arch(hidden_size=k, intermediate_size=n)
+    mlp = px.MLP(arch, px.DecoderOps.with_matmul("fp8"), dtype=torch.bfloat16)
+    for i, name in enumerate(("gate_proj", "up_proj", "down_proj")):
+        o, kk = (k, n) if name == "down_proj" else (n, k)
+        q, s = px.quantize_fp8_block(torch.randn(o, kk, generator=torch.Generator().manual_seed(30 + i)) * 0.03)
+        getattr(mlp, name)._load_from_state_dict({f"{name}.fp8_weight": q, f"{name}.fp8_scale": s.clone()},
+                                                  f"{name}.", {}, True, [], [], [])
+    calls.clear()
+    y = mlp(x)
+    names = [name for name, _ in calls]
+    assert names.count("hn_block_gemm") == 2 and "hn_block_linear" not in names  # the fused pair of GEMMs
+    unfused = mlp.down_proj(F.silu(mlp.gate_proj(x)) * mlp.up_proj(x))
+    assert torch.equal(y, unfused)

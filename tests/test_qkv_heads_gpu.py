@@ -73,6 +73,7 @@ def test_qkv_heads_two_streams_share_one_buffer(dev):
     qt, st = kernels.quantize_activations(xt, "fp8")
     wt, sblk = pixelumm.quantize_fp8_block(torch.randn(3 * hidden, k, generator=g) * 0.02)
     wt, sblk = wt.to(dev), sblk.to(dev)
+    assert kernels.validate_scales(sblk)  # read as stored by the GEMM
     wq = torch.ones(128, device=dev)
     wk = (torch.rand(128, generator=g) + 0.5).to(dev)
     rope = tuple(t.to(dev) for t in rope_tables(g, li))
@@ -109,6 +110,7 @@ def test_qkv_heads_vt_matches_head_major(dev, layout):
     qt, st = kernels.quantize_activations(xt, "fp8")
     wt, sblk = pixelumm.quantize_fp8_block(torch.randn(3 * hidden, k, generator=g) * 0.02)
     wt, sblk = wt.to(dev), sblk.to(dev)
+    assert kernels.validate_scales(sblk)  # read as stored by the GEMM
     wq = (torch.rand(128, generator=g) + 0.5).to(dev)
     wk = (torch.rand(128, generator=g) + 0.5).to(dev)
     rope = tuple(t.to(dev) for t in rope_tables(g, li))

@@ -17,8 +17,12 @@ pytestmark = pytest.mark.gpu
 def fp8_block_weight(g, rows, cols, dev, scale=0.02):
     from hy_nomas import pixelumm
 
+    from hy_nomas import kernels
+
     q, s = pixelumm.quantize_fp8_block(torch.randn(rows, cols, generator=g) * scale)
-    return q.to(dev), s.to(dev)
+    q, s = q.to(dev), s.to(dev)
+    assert kernels.validate_scales(s)  # the device copy: read as stored by every GEMM of the comparison
+    return q, s
 
 
 def unfused(x, gate, up, kind="fp8", group=128):
