@@ -65,7 +65,7 @@ template <int DT, int NORM, bool QUANT, int ROUND, int CPL, bool FULL, bool PT>
 __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ shift,
                                                             const uint16_t* __restrict__ scale, int64_t L,
-                                                            int64_t D, float eps, int blocks_per_batch,
+                                                            int64_t D, float rd, float eps, int blocks_per_batch,
                                                             uint16_t* __restrict__ y, int8_t* __restrict__ q,
                                                             float* __restrict__ s) {
   extern __shared__ float4 fac[];
@@ -95,17 +95,35 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
     float sc[8], sh[8], g[8];
     widen8<DT>(*reinterpret_cast<const uint4*>(scale + b * D + c * 8), sc);
     widen8<DT>(*reinterpret_cast<const uint4*>(shift + b * D + c * 8), sh);
+    // g = rbf16(1 + scale) is finite exactly when scale is (1 + the largest bf16 rounds back to it)
+    bool f = true;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      g[j] = rbf16(1.0f + sc[j]);
-      fin &= __builtin_isfinite(g[j]) && __builtin_isfinite(sh[j]);
+    for (int j = 0; j < 8; j++) f = f && __builtin_isfinite(sc[j]) && __builtin_isfinite(sh[j]);
+    if (f) {  // no NaN: the hardware conversion is the software rounding
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const uint32_t w = bf16x2_finite(1.0f + sc[j], 1.0f + sc[j + 1]);
+        g[j] = __uint_as_float(w << 16);
+        g[j + 1] = __uint_as_float(w & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) g[j] = rbf16(1.0f + sc[j]);
     }
+    fin &= f;
     fac[c] = make_float4(g[0], g[1], g[2], g[3]);
     fac[nchunk + c] = make_float4(g[4], g[5], g[6], g[7]);
     fac[2 * nchunk + c] = make_float4(sh[0], sh[1], sh[2], sh[3]);
     fac[3 * nchunk + c] = make_float4(sh[4], sh[5], sh[6], sh[7]);
   }
-  const bool fac_finite = __syncthreads_and(fin);
+  // Block-wide AND of the staging threads' finiteness: each wave's vote goes to one byte past the factor
+  // planes, so a single barrier publishes both the planes and the votes.
+  uint8_t* votes = reinterpret_cast<uint8_t*>(fac + 4 * nchunk);
+  const bool wave_fin = __builtin_amdgcn_ballot_w64(!fin) == 0;
+  if (lane == 0) votes[threadIdx.x >> 6] = wave_fin;
+  __syncthreads();
+  static_assert(kRowWaves == 8, "eight votes are read as one 8-byte word");
+  const bool fac_finite = *reinterpret_cast<const uint64_t*>(votes) == 0x0101010101010101ull;
   if (!live) return;
 
   // Rows of up to 4096 channels are widened once into fp32 registers; wider rows stay packed and are
@@ -137,7 +155,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
       if (has(i))
 #pragma unroll
         for (int j = 0; j < 8; j++) acc += val(i, j);
-    mean = wave_sum_dpp(acc) / (float)D;
+    mean = div_by_const(wave_sum_dpp(acc), (float)D, rd);
   }
   float sq = 0.0f;
 #pragma unroll
@@ -149,8 +167,8 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
         if constexpr (KEEP) f[i][j] = c;
         sq = __builtin_fmaf(c, c, sq);
       }
-  const float var = wave_sum_dpp(sq) / (float)D;
-  const float rstd = 1.0f / __builtin_sqrtf(var + eps);
+  const float var = div_by_const(wave_sum_dpp(sq), (float)D, rd);
+  const float rstd = rsqrt_refined(var + eps);
   const bool finite = fac_finite && __builtin_isfinite(mean) && __builtin_isfinite(rstd);
   if constexpr (QUANT && PT) {
     // one scale per token: y = rbf16(modulated norm) for the whole row, the row absmax, then the codes
@@ -163,11 +181,24 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
         const float4 g0 = fac[c], g1 = fac[nchunk + c], h0 = fac[2 * nchunk + c], h1 = fac[3 * nchunk + c];
         const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
         const float h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        if (__builtin_expect(finite, 1) && DT == HN_DTYPE_BF16) {
+          // finite statistics and factors: no NaN reaches the rounding, so the hardware conversion applies
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const float o = __builtin_fmaf(f[i][j] * rstd, g[j], h[j]);
-          f[i][j] = rbf16(o);
-          peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j]));  // NaN-free, >= 0
+          for (int j = 0; j < 8; j += 2) {
+            const uint32_t w = bf16x2_finite(__builtin_fmaf(f[i][j] * rstd, g[j], h[j]),
+                                             __builtin_fmaf(f[i][j + 1] * rstd, g[j + 1], h[j + 1]));
+            f[i][j] = __uint_as_float(w << 16);
+            f[i][j + 1] = __uint_as_float(w & 0xffff0000u);
+            peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j]));
+            peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j + 1]));
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            const float o = __builtin_fmaf(f[i][j] * rstd, g[j], h[j]);
+            f[i][j] = rbf16(o);
+            peak = __builtin_fmaxf(peak, __builtin_fabsf(f[i][j]));  // NaN-free, >= 0
+          }
         }
       }
     }
@@ -329,16 +360,17 @@ static int launch_adaln(const void* x, const void* shift, const void* scale, int
     return HN_ERR_UNSUPPORTED;
   }
   const unsigned blocks = (unsigned)(B * per_batch);
-  const size_t lds = (size_t)D * 8;  // four planes of D/8 float4
+  const size_t lds = (size_t)D * 8 + 16;  // four planes of D/8 float4, then the waves' finiteness votes
+  const float rd = 1.0f / (float)D;  // correctly rounded: the kernels divide by D with one correction step
 #define HN_CASE(N)                                                                                              \
   if (cpl <= N) {                                                                                               \
     if (D == 512 * N)                                                                                           \
       hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, true, PT>), dim3(blocks), dim3(kRowThreads), lds, \
-                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
+                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, rd, eps, \
                          (int)per_batch, (uint16_t*)y, q, s);                                                   \
     else                                                                                                        \
       hipLaunchKernelGGL((adaln_kernel<DT, NORM, QUANT, ROUND, N, false, PT>), dim3(blocks), dim3(kRowThreads), lds,\
-                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, eps,     \
+                         st, (const uint16_t*)x, (const uint16_t*)shift, (const uint16_t*)scale, L, D, rd, eps, \
                          (int)per_batch, (uint16_t*)y, q, s);                                                   \
     return HN_LAUNCH_CHECK("adaln_kernel");                                                                     \
   }

@@ -106,6 +106,14 @@ __device__ __forceinline__ float div_by_const(float d, float c, float rc) {
   const float e = __builtin_fmaf(-q0, c, d);
   return __builtin_fmaf(e, rc, q0);
 }
+// 1/sqrt(v) from the hardware reciprocal square root (1 ulp) and one Newton step, for row statistics
+// (where the reductions' own order already moves the last bits).  v = +inf gives 0, v = 0 gives +inf and a
+// NaN stays NaN, as 1/sqrt(v).
+__device__ __forceinline__ float rsqrt_refined(float v) {
+  const float r0 = __builtin_amdgcn_rsqf(v);
+  const float h = __builtin_fmaf(-0.5f * v * r0, r0, 0.5f);  // (1 - v r0^2) / 2
+  return __builtin_isfinite(h) ? __builtin_fmaf(r0, h, r0) : r0;
+}
 __device__ __forceinline__ float int8_scale_fast(float peak) { return div_by_const(peak, 127.0f, 1.0f / 127.0f); }
 __device__ __forceinline__ float fp8_scale_fast(float peak) {
   return div_by_const(peak > 1e-12f ? peak : 1e-12f, 448.0f, 1.0f / 448.0f);
