@@ -47,22 +47,88 @@ static int launch_cfg(GemmArgs& a, hipStream_t st) {
   return HN_LAUNCH_CHECK("block_gemm_kernel");
 }
 
+// The rows of a problem, as two launches: a.M rows from row 0 with the big tile, then the rest with a 128 x 128
+// tile.  Tile rows are independent and every output keeps its fold order, so the results do not depend on
+// where the split falls.
+enum class TileSplit { kBig, kSmall, kBoth };
+
+// Which tiles serve an M x N problem whose big tile is bm x bn with `slots` workgroups resident (one round of
+// tiles), and for kBoth the rows the big tile takes.  A persistent grid runs ceil(tiles / slots) rounds of
+// tiles; when the last round would leave more than half of the compute units idle, its rows go to 128 x 128
+// tiles (four per big tile, on every compute unit).  A problem with fewer big tiles than half a round runs on
+// small tiles alone.
+static TileSplit choose_tiles(int64_t M, int64_t N, int bm, int bn, int64_t slots, int64_t* big_rows) {
+  const int64_t tm = (M + bm - 1) / bm, tn = (N + bn - 1) / bn, tiles = tm * tn;
+  const int64_t full = tiles / slots, rem = tiles % slots;
+  if (rem == 0 || rem > slots / 2) return TileSplit::kBig;
+  if (full == 0) return TileSplit::kSmall;
+  const int64_t rows = (full * slots / tn) * bm;  // whole tile rows of the full rounds
+  if (rows <= 0 || rows >= M) return TileSplit::kBig;
+  *big_rows = rows;
+  return TileSplit::kBoth;
+}
+
+// Launch the big-tile configuration BIG or the small one SMALL (each a launch_cfg instantiation) over the rows
+// choose_tiles assigns them.
+template <int BM, int BN, int WN, int WM, int WPE, typename Big, typename Small>
+static int launch_split(GemmArgs& a, int out_esz, hipStream_t st, Big big, Small small) {
+  const int64_t slots = (int64_t)cu_count() * (WPE * 4 / (WN * WM));
+  int64_t rows = 0;
+  const TileSplit how = choose_tiles(a.M, a.N, BM, BN, slots, &rows);
+  if (how == TileSplit::kBig) return big(a);
+  if (how == TileSplit::kSmall) return small(a);
+  GemmArgs head = a, tail = a;
+  head.M = rows;
+  tail.M = a.M - rows;
+  tail.qa = a.qa + rows * a.lda;
+  tail.sa = a.sa + rows * a.ldsa;
+  tail.out = static_cast<char*>(a.out) + rows * a.ldo * out_esz;
+  const int rc = big(head);
+  return rc != HN_OK ? rc : small(tail);
+}
+
 // per-token / per-channel: 256 x 256 tile, 8 waves of 128 x 64.  fp8 with block weight scales: the same
 // tile (the running sum is rescaled in place, so there is no second accumulator set).  Other g128 layouts:
 // 256 x 128, 8 waves of 128 x 32 (the int32 group partial and the fp32 running sum both fit in 256
-// VGPRs).  128-byte K stages in two LDS buffers.
+// VGPRs).  128-byte K stages in two LDS buffers.  The plain and GELU epilogues also have 128 x 128 tiles of
+// four waves (64 x 64 each, or 128 x 32 with block weight scales) for problems, or tails of problems, that
+// would leave most compute units idle with the big tile (choose_tiles); two such workgroups share a compute
+// unit (about 70 KB of LDS each).
 template <int KIND, int EPI, int OUT_DT>
 static int launch_group(GemmArgs& a, bool g128, hipStream_t st) {
   constexpr bool SWIGLU = EPI == HN_EPI_SWIGLU_QUANT;
-  if (!g128) return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+  constexpr bool SMALL_OK = EPI == HN_EPI_NONE || EPI == HN_EPI_GELU;
+  constexpr int ESZ = OUT_DT == HN_DTYPE_F32 ? 4 : 2;
+  if (!g128) {
+    auto big = [&](GemmArgs& x) { return launch_cfg<KIND, EPI, false, 2, 4, 4, 2, OUT_DT, 128, 2>(x, st); };
+    if constexpr (SMALL_OK) {
+      auto small = [&](GemmArgs& x) { return launch_cfg<KIND, EPI, false, 2, 2, 2, 2, OUT_DT, 128, 2, false, 2>(x, st); };
+      return launch_split<256, 256, 2, 4, 2>(a, ESZ, st, big, small);
+    }
+    return big(a);
+  }
   if constexpr (KIND == HN_KIND_FP8) {
-    if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2, true>(a, st);
+    if (a.sw_rows == 128) {
+      auto big = [&](GemmArgs& x) { return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2, true>(x, st); };
+      if constexpr (SMALL_OK) {
+        auto small = [&](GemmArgs& x) {
+          return launch_cfg<KIND, EPI, true, 1, 4, 4, 1, OUT_DT, 128, 2, true, 2>(x, st);
+        };
+        return launch_split<256, 256, 2, 4, 2>(a, ESZ, st, big, small);
+      }
+      return big(a);
+    }
   }
   if constexpr (!SWIGLU) {
     if constexpr (KIND == HN_KIND_INT8) {  // (fp8 block scales took the branch above)
       if (a.sw_rows == 128) return launch_cfg<KIND, EPI, true, 2, 4, 4, 1, OUT_DT, 128, 2, true>(a, st);
     }
-    return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2>(a, st);
+    auto big = [&](GemmArgs& x) { return launch_cfg<KIND, EPI, true, 2, 4, 4, 2, OUT_DT, 128, 2>(x, st); };
+    if constexpr (SMALL_OK) {
+      auto small = [&](GemmArgs& x) { return launch_cfg<KIND, EPI, true, 2, 2, 2, 2, OUT_DT, 128, 2, false, 2>(x, st); };
+      return launch_split<256, 256, 2, 4, 2>(a, ESZ, st, big, small);
+    }
+    return big(a);
   }
   set_error("hn_block_gemm: swiglu_quant needs per-token scales or fp8 with 128 x 128 block weight scales");
   return HN_ERR_UNSUPPORTED;

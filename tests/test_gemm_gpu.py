@@ -563,3 +563,46 @@ def test_fp8_block_dispatch_does_not_synchronize(dev):
     stored = kernels.block_gemm(qa, sa, qw, sblk_dev, bias, torch.float32, kind="fp8")
     assert not torch.equal(stored, want)  # the rescaled running sum rounds differently...
     assert max_abs_rel(stored.cpu().numpy(), want.cpu().numpy()) < 4e-3  # ...within the fp8 tolerance
+
+
+@pytest.mark.parametrize("layout", ["per_token", "g128", "fp8_block"])
+def test_big_tiles_with_a_small_tile_tail(dev, layout):
+    """A problem whose last round of 256 x 256 tiles would leave most compute units idle: M = 26400, N = 2048
+    makes 832 such tiles (3 rounds and a quarter on 256 compute units), so the first 24576 rows run on big tiles
+    and the rest on 128 x 128 tiles in a second launch.  Rows on both sides of the split, one in every 256-row
+    tile, equal the oracle bit for bit (int8) or within the fp8 tolerance; the GELU epilogue takes the same
+    split."""
+    from hy_nomas import kernels, pixelumm
+
+    m, k, n = 26400, 512, 2048
+    print(f"tile split {layout} m={m} k={k} n={n}", flush=True)
+    g = seeded(2640)
+    x = outlier_input(m, k, seed=2641)
+    split = 24576
+    rows = sorted(set(list(range(0, m, 256)) + [255, 256, split - 257, split - 256, split - 1, split, split + 1,
+                                                split + 127, split + 128, m - 129, m - 128, m - 2, m - 1]))
+    if layout == "fp8_block":
+        qw, sblk = pixelumm.quantize_fp8_block(torch.randn(n, k, generator=g) * 0.02)
+        bias = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+        qa, sa = kernels.quantize_activations(x.to(dev), "fp8")
+        sblk_dev = sblk.to(dev)
+        assert kernels.validate_scales(sblk_dev)
+        out = kernels.block_gemm(qa, sa, qw.to(dev), sblk_dev, bias.to(dev), torch.float32, kind="fp8")
+        sw_full = sblk.repeat_interleave(128, 0).contiguous().numpy()
+        ref = oracle.block_gemm(qa[rows].view(torch.uint8).cpu().numpy(), sa[rows].cpu().numpy(),
+                                qw.view(torch.uint8).numpy(), sw_full, oracle.to_f32(bias), kind="fp8")
+        assert max_abs_rel(out[rows].cpu().numpy(), ref) < 4e-3
+        return
+    w, sw, bias = int8_weights(n, k, seed=2642, per_channel=layout == "per_token")
+    qa, sa = kernels.quantize_activations(x.to(dev), "int8", None if layout == "per_token" else 128)
+    args = (qa, sa, w.to(dev), sw.to(dev), bias.to(dev))
+    out = kernels.block_gemm(*args, torch.float32)
+    ref = oracle.block_gemm(qa[rows].cpu().numpy(), sa[rows].cpu().numpy(), w.numpy(), sw.numpy(), oracle.to_f32(bias))
+    got = out[rows].cpu().numpy()
+    assert np.array_equal(got, ref), f"{int((got != ref).sum())} outputs differ in the sampled rows"
+    out16 = kernels.block_gemm(*args)
+    assert torch.equal(out16[rows].cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+    gelu = kernels.block_gemm(*args, epilogue="gelu")[rows].cpu()
+    ref_gelu = torch.from_numpy(oracle.block_gemm(qa[rows].cpu().numpy(), sa[rows].cpu().numpy(), w.numpy(),
+                                                  sw.numpy(), oracle.to_f32(bias), epilogue="gelu")).to(torch.bfloat16)
+    assert (gelu != ref_gelu).float().mean().item() < 1e-3
