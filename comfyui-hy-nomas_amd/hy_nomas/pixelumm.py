@@ -134,6 +134,9 @@ def _load_fp8_pair(lin, state_dict, prefix, missing_keys):
     if q is None and w is None:
         missing_keys.append(prefix + "weight")
         return None
+    if q is not None and s is None:
+        missing_keys.append(prefix + "fp8_scale")
+        return None
     if q is not None:
         s = s.float()
         _scales_ok(lin, s)
@@ -317,7 +320,8 @@ class MLP(torch.nn.Module):
         return parts if _scales_ok(lin, parts[1]) else None
 
     def _fused_weights(self, device, gate, up):
-        key = (device, gate[0].data_ptr(), up[0].data_ptr(), gate[1]._version, up[1]._version)
+        key = (device, gate[0].data_ptr(), up[0].data_ptr(), gate[0]._version, up[0]._version, gate[1]._version,
+               up[1]._version)
         if self._fused is None or self._fused[0] != key:
             q, s = interleave_gate_up((gate[0].to(device), gate[1].to(device)), (up[0].to(device), up[1].to(device)))
             kernels.trust_scales(s)  # both sources passed the check

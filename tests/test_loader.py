@@ -188,3 +188,8 @@ def test_decoder_mlp_dequant_path_is_the_reference_expression():
         torch.nn.functional.silu(torch.nn.functional.linear(x, wd["gate_proj"])) *
         torch.nn.functional.linear(x, wd["up_proj"]), wd["down_proj"])
     assert torch.equal(mlp(x), ref)
+    # codes without their block scales are reported as missing
+    missing = []
+    lin = pixelumm.DecoderOps.Linear(256, 384, bias=False)
+    lin._load_from_state_dict({"g.fp8_weight": sd["gate_proj.fp8_weight"]}, "g.", {}, True, missing, [], [])
+    assert missing == ["g.fp8_scale"] and lin.weight is None

@@ -291,6 +291,10 @@ def test_comfyui_decoder_linear_loads_the_fp8_layout_and_dequantizes(comfy_pixel
     missing = []
     px.DecoderOps.Linear(k, n)._load_from_state_dict({}, "p.", {}, True, missing, [], [])
     assert missing == ["p.weight"]
+    # codes without their block scales are reported, not loaded
+    missing, no_scale = [], px.DecoderOps.Linear(k, n)
+    no_scale._load_from_state_dict({"p.fp8_weight": q}, "p.", {}, True, missing, [], [])
+    assert missing == ["p.fp8_scale"] and no_scale.weight is None
 
 
 @pytest.mark.gpu
