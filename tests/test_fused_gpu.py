@@ -63,6 +63,56 @@ def test_adaln_quant(dev, b, l, d, norm):
     assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-3)
 
 
+@pytest.mark.parametrize("d,group,norm", [(128, 128, "layer"), (384, None, "rms"), (640, 128, "rms"),
+                                          (640, None, "layer"), (1152, 128, "layer"), (4096, None, "layer")])
+def test_adaln_quant_widths(dev, d, group, norm):
+    """adaLN + int8 quant at widths off the 512-multiple chunk schedule (one or a few 128-channel groups a
+    row) and with one scale per token, against the oracle: codes mismatch < 1e-3 and one step at most, scales
+    within one bf16 ulp of the group peak (the reduction order moves a few modulated values by an ulp)."""
+    from hy_nomas import kernels
+
+    b, l = 2, 97
+    print(f"adaln_quant widths d={d} group={group} norm={norm}", flush=True)
+    g = seeded(7 * d + (group is None))
+    x = bf(torch.randn(b, d, l, generator=g) * 3).transpose(1, 2)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), norm=norm, group=group)
+    q_ref, s_ref, y = oracle.adaln(x.contiguous(), shift, scale, norm=norm, quant=True)
+    if group is None:
+        q_ref, s_ref = oracle.quantize(y, d)
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    assert s.shape == s_ref.shape
+    assert (q != q_ref).mean() < 1e-3
+    assert np.abs(q.astype(np.int32) - q_ref.astype(np.int32)).max() <= 1
+    assert np.abs(s / s_ref - 1).max() <= 2 ** -7
+
+
+def test_adaln_nonfinite_factors(dev):
+    """inf and NaN in the shift / scale factors (the block stages them with the software bf16 rounding): the
+    outputs' NaN and inf positions equal the oracle's, NaNs carry torch's code 0x7FC0, and the finite outputs
+    keep the usual tolerance."""
+    from hy_nomas import fused
+
+    b, l, d = 2, 33, 640
+    g = seeded(31)
+    x = bf(torch.randn(b, d, l, generator=g) * 3).transpose(1, 2)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    scale[0, 5] = float("inf")
+    scale[1, 100] = -float("inf")
+    shift[1, 9] = float("nan")
+    got = fused.adaln(x.to(dev), shift.to(dev), scale.to(dev)).cpu()
+    ref = bf(torch.from_numpy(oracle.adaln(x.contiguous(), shift, scale)).view(b, l, d))
+    assert torch.equal(got.isnan(), ref.isnan()) and torch.equal(got.isinf(), ref.isinf())
+    assert got.isnan().any() and got.isinf().any()
+    assert (got.view(torch.int16)[got.isnan()] == 0x7FC0).all()
+    fin = torch.isfinite(ref)
+    assert torch.equal(got[got.isinf()], ref[ref.isinf()])
+    assert (got[fin] != ref[fin]).float().mean().item() < 1e-3
+    assert (got[fin].float() - ref[fin].float()).abs().max().item() < 0.05
+
+
 def test_adaln_quant_matches_unfused(dev):
     """hy_nomas tests/test_fused.py:52-60."""
     from hy_nomas import fused, kernels
