@@ -1,11 +1,11 @@
 """A seeded sweep of GEMM shapes against the oracle (hy_nomas/kernels.py:80-170): token counts from one row
 (the skinny kernel) through tile edges (127-129, 255-257, 511-513) to several rounds of tiles (the small-tile
 tail of `choose_tiles` at many remainders), channel counts that are and are not multiples of 8 (the LDS-staged
-and the direct bf16 stores), K from one group to 32, per-token and g128 int8 and fp8 with 128 x 128 block
-scales (with a partial last block of channels), with and without bias, bf16 and fp32 outputs, and the GELU
-epilogue.  Rows are independent, so each case checks the rows around every 256-row tile boundary and 40 random
-rows against the oracle on those rows: bit for bit for int8 (GELU: the reference test's tolerance), within 4e-3 of
-the oracle and 1e-2 of the fp64 product for fp8."""
+and the direct 2-byte stores), K from one group to 32, per-token and g128 int8 and fp8 with 128 x 128 block
+scales (with a partial last block of channels), with and without bias, the GELU epilogue, and bf16, fp16 and
+fp32 outputs.  Rows are independent, so each case checks the rows around every 256-row tile boundary and 40
+random rows against the oracle on those rows: bit for bit for int8 (GELU: the reference test's tolerance),
+within 4e-3 of the oracle and 1e-2 of the fp64 product for fp8."""
 import random
 
 import numpy as np
@@ -31,7 +31,7 @@ def _cases(count=40, seed=2026):
     for i in range(count):
         layout = layouts[i % 3]
         m, n, k = rnd.choice(_M), rnd.choice(_N), rnd.choice(_K)
-        out_dt = rnd.choice(["bf16", "f32"])
+        out_dt = rnd.choice(["bf16", "f16", "f32"])
         bias = rnd.random() < 0.75
         gelu = layout != "fp8_block" and rnd.random() < 0.25
         out.append(pytest.param(layout, m, n, k, out_dt, bias, gelu, i,
@@ -52,7 +52,7 @@ def test_gemm_shape_sweep(dev, layout, m, n, k, out_dt, with_bias, gelu, case):
     print(f"sweep case {case}: {layout} M={m} N={n} K={k} out={out_dt} bias={with_bias} gelu={gelu}", flush=True)
     rnd = random.Random(case)
     g = seeded(1000 + case)
-    out_dtype = torch.bfloat16 if out_dt == "bf16" else torch.float32
+    out_dtype = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[out_dt]
     x = outlier_input(m, k, seed=2000 + case)
     rows = _rows(m, rnd)
     if layout == "fp8_block":
@@ -86,7 +86,7 @@ def test_gemm_shape_sweep(dev, layout, m, n, k, out_dt, with_bias, gelu, case):
                             epilogue="gelu" if gelu else None)
     ref = torch.from_numpy(ref).to(out_dtype)
     if not gelu:
-        bits = (lambda t: t.view(torch.int16)) if out_dtype == torch.bfloat16 else (lambda t: t.view(torch.int32))
+        bits = (lambda t: t.view(torch.int32)) if out_dtype == torch.float32 else (lambda t: t.view(torch.int16))
         diff = (bits(got) != bits(ref)).nonzero()
         assert diff.numel() == 0, f"{len(diff)} outputs differ, first (row index, channel) {diff[:3].tolist()}"
     else:
