@@ -140,6 +140,9 @@ void attention_kernel(const AttnArgs a) {
   const float inv_scale = 1.0f / a.scale_log2;
   float mref_m = 0.0f;  // the reference mref holds (m', base-2 units)
   float lsum = 0.0f;            // this lane's partial sum of the probabilities
+  float psum[16];               // the last tile's probability pair sums, not yet in lsum
+#pragma unroll
+  for (int i = 0; i < 16; i++) psum[i] = 0.0f;
   const int kswz = l32 & 15, vswz = (l32 >> 1) & 7;   // the lane's rows' swizzles (rows 32 i + l32)
 
   const int64_t nt = (a.Lk + kBK - 1) / kBK;
@@ -179,6 +182,11 @@ void attention_kernel(const AttnArgs a) {
         read_k(ks + 2, kf[(ks + 2) % 3]);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
+      // the previous tile's probability sums join the running sum while the matrix core works (the
+      // reference m' has not moved since they were formed: a move below rescales lsum after this)
+      lsum += psum[2 * ks];
+      lsum += psum[2 * ks + 1];
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
     }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
       // register r of block kb holds key j0 + 32 kb + 8 (r / 4) + (r % 4) + 4 h2: a constant per register
@@ -230,7 +238,7 @@ void attention_kernel(const AttnArgs a) {
       for (int p = 0; p < 8; p++) {
         const float e0 = __builtin_amdgcn_exp2f(s[kb][2 * p] * a.scale_log2);
         const float e1 = __builtin_amdgcn_exp2f(s[kb][2 * p + 1] * a.scale_log2);
-        lsum += e0 + e1;
+        psum[8 * kb + p] = e0 + e1;
         pk[kb][p] = bf16x2_finite(e0, e1);
       }
     // O^T += V^T P^T over the four 16-key groups g = 2 kb + ks2: the B fragment is score registers
@@ -254,6 +262,8 @@ void attention_kernel(const AttnArgs a) {
     tile(t, std::integral_constant<int, 0>());
     if (t + 1 < nt) tile(t + 1, std::integral_constant<int, 1>());
   }
+#pragma unroll
+  for (int i = 0; i < 16; i++) lsum += psum[i];
   // normalize and store: lane holds query l32, dims 32 db + 8 rr + 4 h2 + 0..3 in registers 4 rr .. 4 rr + 3
   const float ltot = lsum + __shfl_xor(lsum, 32);
   const float inv = 1.0f / ltot;
