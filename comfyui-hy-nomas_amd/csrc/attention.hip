@@ -140,9 +140,9 @@ void attention_kernel(const AttnArgs a) {
   const float inv_scale = 1.0f / a.scale_log2;
   float mref_m = 0.0f;  // the reference mref holds (m', base-2 units)
   float lsum = 0.0f;            // this lane's partial sum of the probabilities
-  float psum[16];               // the last tile's probability pair sums, not yet in lsum
+  float pv[32];                 // the last tile's probabilities, not yet in lsum
 #pragma unroll
-  for (int i = 0; i < 16; i++) psum[i] = 0.0f;
+  for (int i = 0; i < 32; i++) pv[i] = 0.0f;
   const int kswz = l32 & 15, vswz = (l32 >> 1) & 7;   // the lane's rows' swizzles (rows 32 i + l32)
 
   const int64_t nt = (a.Lk + kBK - 1) / kBK;
@@ -184,9 +184,9 @@ void attention_kernel(const AttnArgs a) {
       }
       // the previous tile's probability sums join the running sum while the matrix core works (the
       // reference m' has not moved since they were formed: a move below rescales lsum after this)
-      lsum += psum[2 * ks];
-      lsum += psum[2 * ks + 1];
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) lsum += pv[4 * ks + i];
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
     }
     if (j0 + kBK > a.Lk) {  // the last tile: keys past the end take no weight
       // register r of block kb holds key j0 + 32 kb + 8 (r / 4) + (r % 4) + 4 h2: a constant per register
@@ -238,7 +238,8 @@ void attention_kernel(const AttnArgs a) {
       for (int p = 0; p < 8; p++) {
         const float e0 = __builtin_amdgcn_exp2f(s[kb][2 * p] * a.scale_log2);
         const float e1 = __builtin_amdgcn_exp2f(s[kb][2 * p + 1] * a.scale_log2);
-        psum[8 * kb + p] = e0 + e1;
+        pv[16 * kb + 2 * p] = e0;
+        pv[16 * kb + 2 * p + 1] = e1;
         pk[kb][p] = bf16x2_finite(e0, e1);
       }
     // O^T += V^T P^T over the four 16-key groups g = 2 kb + ks2: the B fragment is score registers
@@ -263,7 +264,7 @@ void attention_kernel(const AttnArgs a) {
     if (t + 1 < nt) tile(t + 1, std::integral_constant<int, 1>());
   }
 #pragma unroll
-  for (int i = 0; i < 16; i++) lsum += psum[i];
+  for (int i = 0; i < 32; i++) lsum += pv[i];
   // normalize and store: lane holds query l32, dims 32 db + 8 rr + 4 h2 + 0..3 in registers 4 rr .. 4 rr + 3
   const float ltot = lsum + __shfl_xor(lsum, 32);
   const float inv = 1.0f / ltot;
