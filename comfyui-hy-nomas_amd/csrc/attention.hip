@@ -182,7 +182,7 @@ void attention_kernel(const AttnArgs a) {
         read_k(ks + 2, kf[(ks + 2) % 3]);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
-      // the previous tile's probability sums join the running sum while the matrix core works (the
+      // the previous tile's probabilities join the running sum while the matrix core works (the
       // reference m' has not moved since they were formed: a move below rescales lsum after this)
 #pragma unroll
       for (int i = 0; i < 4; i++) lsum += pv[4 * ks + i];
