@@ -1,7 +1,7 @@
 """CPU parity oracle for the quantized DiT linear path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
-package, and only as the checker (or, for the baseline, as the timed CPU restatement).  The product
+package, and only to check the product's results (or, for the baseline, as the timed CPU restatement).  The product
 package never imports it.
 
 The arithmetic lives in ``hn_oracle.c`` (compiled by ``oracle/build.py`` into ``liboracle.so``).  This

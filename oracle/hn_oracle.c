@@ -2,7 +2,7 @@
  * CPU restatement of Hy-Nomas' quantized DiT linear path (TEST INFRASTRUCTURE ONLY).
  *
  * This file is the parity oracle.  Only tests/, __graft_entry__.smoke() and
- * bench.py's cpu_baseline leg may load it, and only as the checker.  The
+ * bench.py's cpu_baseline leg may load it, and only to check results.  The
  * product path (comfyui-hy-nomas_amd/) never links or calls it.
  *
  * Every float operation is written out in the order the reference evaluates

@@ -1,6 +1,6 @@
 """Torch restatements of the reference's DiT block arithmetic -- TEST INFRASTRUCTURE ONLY.
 
-Like the rest of ``oracle/``, only ``tests/`` import this module, as the checker; the product package never
+Like the rest of ``oracle/``, only ``tests/`` import this module, to check results; the product package never
 does.  These are the reference's non-fused torch forms that its fused kernels replace, and the float32
 "exact-matmul" double-stream block the int8 path is compared against:
 
