@@ -40,6 +40,28 @@ def test_attention_matches_float32(dev, b, h, lq, lk, mag):
     assert fro_s < 1e-2, fro_s
 
 
+@pytest.mark.parametrize("lk", [1000, 4096])
+def test_attention_growing_scores(dev, lk):
+    """Keys whose scale grows along the sequence, so the tile max rises tile after tile and the lazy
+    reference moves many times (each move rescales the running sums after the previous tile's probabilities
+    have joined them), and a last block of keys far above the rest (a late jump of the reference): against
+    float32 softmax attention at the usual tolerances."""
+    from hy_nomas import attention
+
+    print(f"attention growing scores lk={lk}", flush=True)
+    g = seeded(lk + 3)
+    b, h, lq = 1, 2, 160
+    q = torch.randn(b, lq, h, 128, generator=g)
+    k = torch.randn(b, lk, h, 128, generator=g) * torch.linspace(0.2, 3.0, lk).view(1, lk, 1, 1)
+    k[:, -40:] *= 2.5
+    v = torch.randn(b, lk, h, 128, generator=g)
+    q, k, v = (t.to(torch.bfloat16).to(dev) for t in (q, k, v))
+    got = attention.attention(q, k, v, backend="hip")
+    assert torch.isfinite(got.float()).all()
+    fro, mx = rel(got, ref_attention(q, k, v))
+    assert fro < 1e-2 and mx < 3e-2, (fro, mx)
+
+
 def test_attention_heads_on_strided_qkv(dev):
     """Head-major q, k, v as views of one [3, B, H, L, 128] buffer (the QKV epilogue's output)."""
     from hy_nomas import attention
