@@ -594,7 +594,12 @@ void block_gemm_kernel(const GemmArgs a) {
         const float swp = sp[wn * TN * 32], swc = sc[wn * TN * 32];
 #pragma unroll
         for (int j = 0; j < TM; j++) {
-          const float rho = (sp[BN + wrow_m + j * 32] * swp) / (sc[BN + wrow_m + j * 32] * swc);
+          // the ratio from the hardware reciprocal with one Newton step (within an ulp or two of the quotient;
+          // the running sum rounds once per group anyway)
+          const float den = sc[BN + wrow_m + j * 32] * swc;
+          const float r0 = __builtin_amdgcn_rcpf(den);
+          const float r = __builtin_fmaf(__builtin_fmaf(-den, r0, 1.0f), r0, r0);
+          const float rho = (sp[BN + wrow_m + j * 32] * swp) * r;
           rs[j] = kt > 0 ? rho : 1.0f;
         }
       }
