@@ -498,7 +498,9 @@ void block_gemm_kernel(const GemmArgs a) {
     // ---- main loop of tile (m0, n0); its stage 0 is in flight into buffer 0
     Acc acc[TN][TM];                            // MFMA accumulators (whole K, or one group in g128 mode)
     v16f facc[G128 && !RESCALE ? TN : 1][G128 && !RESCALE ? TM : 1];  // g128: fp32 running sum over groups
-    float ss_last[TM];                          // RESCALE: the last group's scale product per token
+    float ss_last[TM];                          // RESCALE: the latest group's scale product per token
+#pragma unroll
+    for (int j = 0; j < TM; j++) ss_last[j] = 1.0f;
 #pragma unroll
     for (int i = 0; i < TN; i++)
 #pragma unroll
@@ -583,24 +585,23 @@ void block_gemm_kernel(const GemmArgs a) {
     auto stage_body = [&](int kt, int buf, auto mode_c) __attribute__((always_inline)) {
       constexpr int MODE = decltype(mode_c)::value;
       const char* stage = smem + SCR + buf * STAGE;
-      // RESCALE: the factor from the previous group's scale product to this one's (1 at the tile's first
-      // stage).  The previous group's scales are still in their ring slot: stage kt + 2 refills it only
-      // after this stage's barrier.
+      // RESCALE: the factor from the previous group's scale product (carried from the previous stage) to this
+      // one's (1 at the tile's first stage).
       float rs[TM];
       if constexpr (RESCALE) {
         static_assert(STAGES_PER_GROUP == 1, "one group per stage");
-        const float* sp = reinterpret_cast<const float*>(smem + ((kt + NS) % (NS + 1)) * SC_BYTES);
         const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
-        const float swp = sp[wn * TN * 32], swc = sc[wn * TN * 32];
+        const float swc = sc[wn * TN * 32];  // the wave's one weight scale
 #pragma unroll
         for (int j = 0; j < TM; j++) {
-          // the ratio from the hardware reciprocal with one Newton step (within an ulp or two of the quotient;
-          // the running sum rounds once per group anyway)
+          // this group's scale product; the previous group's is carried in ss_last.  The ratio comes from the
+          // hardware reciprocal with one Newton step (within an ulp or two of the quotient; the running sum
+          // rounds once per group anyway)
           const float den = sc[BN + wrow_m + j * 32] * swc;
           const float r0 = __builtin_amdgcn_rcpf(den);
           const float r = __builtin_fmaf(__builtin_fmaf(-den, r0, 1.0f), r0, r0);
-          const float rho = (sp[BN + wrow_m + j * 32] * swp) * r;
-          rs[j] = kt > 0 ? rho : 1.0f;
+          rs[j] = kt > 0 ? ss_last[j] * r : 1.0f;
+          ss_last[j] = den;
         }
       }
 #pragma unroll
@@ -642,12 +643,7 @@ void block_gemm_kernel(const GemmArgs a) {
         }
       }
       if constexpr (RESCALE) {
-        if constexpr (MODE == 2) {
-          const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
-          const float swb = sc[wn * TN * 32];  // the wave's one weight scale
-#pragma unroll
-          for (int j = 0; j < TM; j++) ss_last[j] = sc[BN + wrow_m + j * 32] * swb;
-        }
+        // (ss_last holds this group's scale product: after the last stage, the epilogue's factor)
       } else if constexpr (G128) {
         if ((kt + 1) % STAGES_PER_GROUP == 0) {
           const float* sc = reinterpret_cast<const float*>(smem + (kt % (NS + 1)) * SC_BYTES);
