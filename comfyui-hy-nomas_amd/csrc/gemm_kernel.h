@@ -862,14 +862,23 @@ void block_gemm_kernel(const GemmArgs a) {
             const float4 b4 = *reinterpret_cast<const float4*>(ep + BN + nloc + i * 32 + rr * 8);
             const float swq[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
             const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+            // bf16 rounding two at a time with the hardware pack: rbf16 for every non-NaN value, and a NaN
+            // stays a NaN of its sign (as under rbf16, bar the top payloads, which it carries into a zero);
+            // the codes below read at most that sign (the peak skips NaN)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const int r = rr * 4 + q;
-              float v;
-              if constexpr (RESCALE) v = MF::get(acc[i][j], r) * ss_last[j];
-              else if constexpr (G128) v = facc[i][j][r];
-              else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
-              MF::put(acc[i][j], r, rbf16(v + bq[q]));
+            for (int q = 0; q < 4; q += 2) {
+              float v[2];
+#pragma unroll
+              for (int t = 0; t < 2; t++) {
+                const int r = rr * 4 + q + t;
+                if constexpr (RESCALE) v[t] = MF::get(acc[i][j], r) * ss_last[j];
+                else if constexpr (G128) v[t] = facc[i][j][r];
+                else v[t] = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q + t], 0.0f);
+                v[t] = v[t] + bq[q + t];
+              }
+              const uint32_t pb = bf16x2_finite(v[0], v[1]);
+              MF::put(acc[i][j], rr * 4 + q, __uint_as_float(pb << 16));
+              MF::put(acc[i][j], rr * 4 + q + 1, __uint_as_float(pb & 0xffff0000u));
             }
           }
         }
@@ -898,7 +907,10 @@ void block_gemm_kernel(const GemmArgs a) {
       else send(std::integral_constant<int, 0>());
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       barrier();
-      // h = bf16(bf16(silu(g)) * u), then the codes of each token's 128-channel group (lanes l and l^32)
+      // h = bf16(bf16(silu(g)) * u), then the codes of each token's 128-channel group (lanes l and l^32).
+      // Pairs of values share one hardware bf16 pack; the fp8 per-channel variant keeps one value at a
+      // time, since its paired form does not fit the register file.
+      constexpr bool PAIRED = !(KIND == HN_KIND_FP8 && !RESCALE);
       auto finish = [&](auto jc, auto gate_c) __attribute__((always_inline)) {
         constexpr int J0 = decltype(jc)::value;
         constexpr bool OWN_GATE = decltype(gate_c)::value;
@@ -912,16 +924,36 @@ void block_gemm_kernel(const GemmArgs a) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
               const v4i p = *reinterpret_cast<const v4i*>(pslot + ((jj * TN + i) * 2 + h) * 1024);
+              if constexpr (!PAIRED) {
 #pragma unroll
-              for (int e = 0; e < 8; e++) {
+                for (int e = 0; e < 8; e++) {
+                  const int r = h * 8 + e;
+                  const uint32_t pw = (uint32_t)p[e >> 1];
+                  const float other = __uint_as_float((e & 1) ? (pw & 0xffff0000u) : (pw << 16));
+                  const float own = MF::get(acc[i][J0 + jj], r);
+                  const float g = OWN_GATE ? own : other, u = OWN_GATE ? other : own;
+                  const float hv = rbf16(silu_bf16(g) * u);
+                  MF::put(acc[i][J0 + jj], r, hv);
+                  peak = __builtin_fmaxf(peak, __builtin_fabsf(hv));
+                }
+                continue;
+              }
+#pragma unroll
+              for (int e = 0; e < 8; e += 2) {
                 const int r = h * 8 + e;
                 const uint32_t pw = (uint32_t)p[e >> 1];
-                const float other = __uint_as_float((e & 1) ? (pw & 0xffff0000u) : (pw << 16));
-                const float own = MF::get(acc[i][J0 + jj], r);
-                const float g = OWN_GATE ? own : other, u = OWN_GATE ? other : own;
-                const float hv = rbf16(silu_bf16(g) * u);
-                MF::put(acc[i][J0 + jj], r, hv);
-                peak = __builtin_fmaxf(peak, __builtin_fabsf(hv));
+                const float other0 = __uint_as_float(pw << 16), other1 = __uint_as_float(pw & 0xffff0000u);
+                const float own0 = MF::get(acc[i][J0 + jj], r), own1 = MF::get(acc[i][J0 + jj], r + 1);
+                const float g0 = OWN_GATE ? own0 : other0, u0 = OWN_GATE ? other0 : own0;
+                const float g1 = OWN_GATE ? own1 : other1, u1 = OWN_GATE ? other1 : own1;
+                float s0, s1;
+                silu_bf16x2(g0, g1, s0, s1);
+                // bf16(silu * up) two at a time with the hardware pack (as above)
+                const uint32_t ph = bf16x2_finite(s0 * u0, s1 * u1);
+                const float hv0 = __uint_as_float(ph << 16), hv1 = __uint_as_float(ph & 0xffff0000u);
+                MF::put(acc[i][J0 + jj], r, hv0);
+                MF::put(acc[i][J0 + jj], r + 1, hv1);
+                peak = __builtin_fmaxf(peak, __builtin_fmaxf(__builtin_fabsf(hv0), __builtin_fabsf(hv1)));
               }
             }
           peak = __builtin_fmaxf(peak, shfl_xor_f(peak, 32));

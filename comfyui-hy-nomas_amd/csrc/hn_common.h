@@ -64,6 +64,22 @@ __device__ __forceinline__ float silu_bf16(float g) {
   return rbf16(f);
 }
 
+// silu_bf16 of two values, the fast path's rounding by the hardware pair conversion (its values are finite,
+// where the pack equals rbf16); lanes that take the slow path (as in silu_bf16) round in software.
+__device__ __forceinline__ uint32_t bf16x2_finite(float a, float b);
+__device__ __forceinline__ void silu_bf16x2(float g0, float g1, float& s0, float& s1) {
+  const float e0 = __builtin_amdgcn_exp2f(g0 * -1.4426950408889634f);
+  const float e1 = __builtin_amdgcn_exp2f(g1 * -1.4426950408889634f);
+  const float f0 = g0 * __builtin_amdgcn_rcpf(1.0f + e0);
+  const float f1 = g1 * __builtin_amdgcn_rcpf(1.0f + e1);
+  const uint32_t p = bf16x2_finite(f0, f1);
+  s0 = __uint_as_float(p << 16);
+  s1 = __uint_as_float(p & 0xffff0000u);
+  const uint32_t l0 = __float_as_uint(f0) & 0xffffu, l1 = __float_as_uint(f1) & 0xffffu;
+  if (__builtin_expect((l0 - 0x7fe0u) < 0x40u || !(g0 >= -16.0f), 0)) s0 = rbf16(silu_f32(g0));
+  if (__builtin_expect((l1 - 0x7fe0u) < 0x40u || !(g1 >= -16.0f), 0)) s1 = rbf16(silu_f32(g1));
+}
+
 // OCP e4m3fn encoding, round to nearest even; values that round past 448 give the NaN code 0x7F.
 __device__ __forceinline__ uint32_t e4m3_encode(float f) {
   uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;

@@ -132,9 +132,10 @@ def test_swiglu_quant_rejects_bad_layouts(dev):
 
 def test_fast_silu_equals_the_reference_for_every_bf16_value(dev):
     """The SwiGLU epilogue's silu of a bf16 value (hardware exponential and reciprocal, the library form near
-    bf16 rounding midpoints and for g < -16) against the fp32 form rounded to bf16, for all 65536 bf16 bit
-    patterns (libhynomas_probes.so: hnp_silu_mismatches), and against torch's silu of the bf16 values on the
-    CPU (the reference's F.silu), NaNs compared as NaNs."""
+    bf16 rounding midpoints and for g < -16), one value at a time and in pairs rounded by the hardware pack,
+    against the fp32 form rounded to bf16, for all 65536 bf16 bit patterns in each slot
+    (libhynomas_probes.so: hnp_silu_mismatches), and against torch's silu of the bf16 values on the CPU
+    (the reference's F.silu), NaNs compared as NaNs."""
     import ctypes
     import os
 
