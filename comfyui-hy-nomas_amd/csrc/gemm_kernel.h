@@ -1009,16 +1009,29 @@ void block_gemm_kernel(const GemmArgs a) {
             const float4 b4 = *reinterpret_cast<const float4*>(ep + BN + nloc + i * 32 + rr * 8);
             const float swq[4] = {sw4.x, sw4.y, sw4.z, sw4.w};
             const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+            constexpr bool GELU = EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT;
+            // GELU: both bf16 roundings two values at a time with the hardware pack (rbf16 for every
+            // non-NaN value; a NaN stays a NaN of its sign)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const int r = rr * 4 + q;
-              float v;
-              if constexpr (RESCALE) v = MF::get(acc[i][j], r) * ss_last[j];
-              else if constexpr (G128) v = facc[i][j][r];
-              else v = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q], 0.0f);
-              v = v + bq[q];
-              if constexpr (EPI == HN_EPI_GELU || EPI == HN_EPI_GELU_QUANT) v = rbf16(gelu_tanh(rbf16(v)));
-              MF::put(acc[i][j], r, v);
+            for (int q = 0; q < 4; q += GELU ? 2 : 1) {
+              float v[2];
+#pragma unroll
+              for (int t = 0; t < (GELU ? 2 : 1); t++) {
+                const int r = rr * 4 + q + t;
+                if constexpr (RESCALE) v[t] = MF::get(acc[i][j], r) * ss_last[j];
+                else if constexpr (G128) v[t] = facc[i][j][r];
+                else v[t] = __builtin_fmaf(MF::to_f32(acc[i][j][r]) * sam, swq[q + t], 0.0f);
+                v[t] = v[t] + bq[q + t];
+              }
+              if constexpr (GELU) {
+                const uint32_t px = bf16x2_finite(v[0], v[1]);
+                const uint32_t pg = bf16x2_finite(gelu_tanh(__uint_as_float(px << 16)),
+                                                  gelu_tanh(__uint_as_float(px & 0xffff0000u)));
+                MF::put(acc[i][j], rr * 4 + q, __uint_as_float(pg << 16));
+                MF::put(acc[i][j], rr * 4 + q + 1, __uint_as_float(pg & 0xffff0000u));
+              } else {
+                MF::put(acc[i][j], rr * 4 + q, v[0]);
+              }
             }
           }
         }
