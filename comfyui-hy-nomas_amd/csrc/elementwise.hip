@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             const float v = div(f[i][j]);
-            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? rne_code_bits(v) : round_half_away_i8_inrange(v);
           }
         } else {
 #pragma unroll
@@ -251,26 +251,34 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
         }
         pk[i] = peak;
       }
-      bool all_fast = true;
 #pragma unroll
-      for (int i = 0; i < CPL; i++) {
-        pk[i] = row16_max_nonneg(pk[i]);  // D % 128 == 0: a DPP row of 16 lanes holds one group
-        all_fast = all_fast && fast_group_i8(pk[i]);
-      }
-      if (__builtin_expect(__all(all_fast), 1)) {
+      for (int i = 0; i < CPL; i++) pk[i] = row16_max_nonneg(pk[i]);  // D % 128 == 0: a DPP row holds one group
+      // Each group's scale and quotient constants are formed once, in lane k < CPL of its 16-lane row (lane k
+      // takes chunk k's group, channels 128 (4k + row) on), and chunk i reads them from lane i of the row with
+      // a DPP broadcast, instead of every lane forming them for each of its chunks; one store then writes the
+      // row's group scales.  The lanes k >= CPL keep chunk 0's group, so the vote covers exactly the groups.
+      static_assert(CPL <= 16, "one lane of the row per chunk");
+      const int k = lane & 15;
+      float pkk = pk[0];
+#pragma unroll
+      for (int i = 1; i < CPL; i++) pkk = k == i ? pk[i] : pkk;
+      if (__builtin_expect(__all(fast_group_i8(pkk)), 1)) {
+        const float gs = int8_scale_fast(pkk);
+        const FastDivI8 div_k(gs);
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
-          const float gs = int8_scale_fast(pk[i]);
-          const FastDivI8 div(gs);
+          FastDivI8 div = div_k;
+          div.r = row_bcast(div_k.r, i);
+          div.rl = row_bcast(div_k.rl, i);
           int cd[8];
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             const float v = div(f[i][j]);
-            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? rne_code_bits(v) : round_half_away_i8_inrange(v);
           }
           st_nt8(qrow + 512 * i, make_uint2(pack4_i8(cd[0], cd[1], cd[2], cd[3]), pack4_i8(cd[4], cd[5], cd[6], cd[7])));
-          srow[4 * i] = gs;
         }
+        if (k < CPL) srow[4 * k] = gs;  // srow[4 k] is group 4 k + row
       } else {
 #pragma unroll
         for (int i = 0; i < CPL; i++) {
@@ -281,7 +289,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
             for (int j = 0; j < 8; j++) {
               const float v = div(f[i][j]);
-              cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+              cd[j] = ROUND == HN_ROUND_HALF_EVEN ? rne_code_bits(v) : round_half_away_i8_inrange(v);
             }
           } else {
 #pragma unroll
@@ -335,7 +343,7 @@ __global__ __launch_bounds__(kRowThreads) void adaln_kernel(const uint16_t* __re
 #pragma unroll
           for (int j = 0; j < 8; j++) {
             const float v = div(o[j]);
-            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? (int)__builtin_rintf(v) : round_half_away_i8_inrange(v);
+            cd[j] = ROUND == HN_ROUND_HALF_EVEN ? rne_code_bits(v) : round_half_away_i8_inrange(v);
           }
         } else {
           gs = int8_scale(peak);

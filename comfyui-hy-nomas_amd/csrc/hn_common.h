@@ -219,6 +219,12 @@ __device__ __forceinline__ int round_i8(float y) {
   else return round_half_away_i8(y);
 }
 
+// The half-even int8 code of y, for |y| <= 127 (1 + 2^-22), as the low byte of the result: adding 1.5 * 2^23
+// rounds y to an integer n, ties to even (the sum's fp32 spacing is 1 and 1.5 * 2^23 is even), leaving the
+// bits 0x4B400000 + n, whose low byte is n's two's-complement byte.  One op instead of rint and a conversion;
+// only the low byte is meaningful, which is all pack4_i8 reads.
+__device__ __forceinline__ int rne_code_bits(float y) { return (int)__float_as_uint(y + 12582912.0f); }
+
 // Pack four int8 codes (low byte first).
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
   const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);  // [a.b0, b.b0, 0, 0]
@@ -296,6 +302,28 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Lane n of each DPP row of 16, read by every lane of the row (row_newbcast); n must fold to a constant.
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  switch (n) {
+    case 0: return dpp_f<0x150>(v);
+    case 1: return dpp_f<0x151>(v);
+    case 2: return dpp_f<0x152>(v);
+    case 3: return dpp_f<0x153>(v);
+    case 4: return dpp_f<0x154>(v);
+    case 5: return dpp_f<0x155>(v);
+    case 6: return dpp_f<0x156>(v);
+    case 7: return dpp_f<0x157>(v);
+    case 8: return dpp_f<0x158>(v);
+    case 9: return dpp_f<0x159>(v);
+    case 10: return dpp_f<0x15A>(v);
+    case 11: return dpp_f<0x15B>(v);
+    case 12: return dpp_f<0x15C>(v);
+    case 13: return dpp_f<0x15D>(v);
+    case 14: return dpp_f<0x15E>(v);
+    default: return dpp_f<0x15F>(v);
+  }
 }
 
 // Max over the 16 lanes of each DPP row of non-negative values (compared as integers: the order of

@@ -48,7 +48,7 @@ __device__ __forceinline__ uint2 encode8(const float* f, float scale) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float y = div(f[i]);
-      if constexpr (ROUND == HN_ROUND_HALF_EVEN) c[i] = (int)__builtin_rintf(y);
+      if constexpr (ROUND == HN_ROUND_HALF_EVEN) c[i] = rne_code_bits(y);  // low byte only: packed below
       else c[i] = round_half_away_i8_inrange(y);
     }
   } else {

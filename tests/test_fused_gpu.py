@@ -215,6 +215,57 @@ def test_adaln_quant_per_token(dev, b, l, d):
     assert np.allclose(s.cpu().numpy(), s_ref, rtol=1e-3)
 
 
+@pytest.mark.parametrize("d,group,norm", [(3072, 128, "layer"), (3072, None, "layer"), (640, 128, "rms"),
+                                          (2048, None, "rms"), (12288, 128, "layer")])
+def test_adaln_quant_half_even(dev, d, group, norm):
+    """adaLN + int8 quant with half-even codes (the rounding the per-token W8A8 path uses) against the oracle's
+    half-even quantization of its own adaLN output: codes mismatch < 1e-3 and one step at most (the statistics'
+    reduction order moves a few modulated values by an ulp), scales within one bf16 ulp."""
+    from hy_nomas import kernels
+
+    b, l = 2, 129
+    print(f"adaln_quant half_even d={d} group={group} norm={norm}", flush=True)
+    g = seeded(11 * d + (group is None) + 3 * (norm == "rms"))
+    x = bf(torch.randn(b, l, d, generator=g) * 3)
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), norm=norm, rounding="half_even", group=group)
+    q_ref, s_ref, y = oracle.adaln(x, shift, scale, norm=norm, quant=True, rounding="half_even")
+    if group is None:
+        q_ref, s_ref = oracle.quantize(y, d, "int8", rounding="half_even")
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    assert s.shape == s_ref.shape
+    assert (q != q_ref).mean() < 1e-3
+    assert np.abs(q.astype(np.int32) - q_ref.astype(np.int32)).max() <= 1
+    assert np.abs(s / s_ref - 1).max() <= 2 ** -7
+
+
+@pytest.mark.parametrize("group", [128, None])
+def test_adaln_quant_subnormal_rows(dev, group):
+    """Rows of bf16 subnormals (|x| < 2^-126) next to ordinary rows, with zero shift and scale: the outputs are
+    the centred values times rstd, so a mean that lost the subnormal terms (a flushed sum) would move every
+    code of those rows.  Against the oracle, whose C arithmetic keeps subnormals: codes one step at most."""
+    from hy_nomas import kernels
+
+    print(f"adaln_quant subnormal rows group={group}", flush=True)
+    g = seeded(4242 + (group is None))
+    b, l, d = 1, 64, 3072
+    x = torch.randn(b, l, d, generator=g)
+    x[:, ::2] *= 2.0 ** -130  # even rows: bf16 subnormals (and zeros)
+    x = bf(x)
+    assert (x[:, ::2].float().abs().max() < 2.0 ** -126) and (x[:, ::2] != 0).float().mean() > 0.9
+    shift = torch.zeros(b, d, dtype=torch.bfloat16)
+    scale = torch.zeros(b, d, dtype=torch.bfloat16)
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), group=group)
+    q_ref, s_ref, y = oracle.adaln(x, shift, scale, quant=True)
+    if group is None:
+        q_ref, s_ref = oracle.quantize(y, d)
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    assert np.abs(q.astype(np.int32) - q_ref.astype(np.int32)).max() <= 1
+    assert (q != q_ref).mean() < 1e-3
+    assert np.abs(s / s_ref - 1).max() <= 2 ** -7
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("b,t,p,d,frame_b", [(1, 3, 5, 3072, 1), (2, 4, 33, 256, 2), (2, 2, 7, 64, 1)])
 def test_gated_residual_frames_matches_two_torch_ops(dev, dtype, b, t, p, d, frame_b):
