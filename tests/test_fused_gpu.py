@@ -113,6 +113,40 @@ def test_adaln_nonfinite_factors(dev):
     assert (got[fin].float() - ref[fin].float()).abs().max().item() < 0.05
 
 
+@pytest.mark.parametrize("group", [128, None])
+def test_adaln_quant_nonfinite(dev, group):
+    """inf and NaN in the factors and in two token rows, quantized: scales against the oracle's quantization of
+    its own adaLN output (the peaks skip NaN; an infinite peak gives an infinite scale), finite scales within
+    one bf16 ulp, and the codes of every finite value one step at most (zero under an infinite peak).  NaN
+    values, and the infinite ones (inf / inf), have no defined code in the reference (its clamp's maximum and
+    minimum ignore NaN where it runs, giving -127; the oracle's C conversion gives 0): they are not compared."""
+    from hy_nomas import kernels
+
+    print(f"adaln_quant nonfinite group={group}", flush=True)
+    b, l, d = 2, 33, 640
+    g = seeded(37 + (group is None))
+    x = bf(torch.randn(b, l, d, generator=g) * 3)
+    x[0, 3, 17] = float("inf")
+    x[1, 7, 300] = float("nan")
+    shift = bf(torch.randn(b, d, generator=g))
+    scale = bf(torch.randn(b, d, generator=g))
+    scale[0, 5] = float("inf")
+    scale[1, 100] = -float("inf")
+    shift[1, 9] = float("nan")
+    q, s = kernels.adaln_quant(x.to(dev), shift.to(dev), scale.to(dev), group=group)
+    q_ref, s_ref, y = oracle.adaln(x, shift, scale, quant=True)
+    if group is None:
+        q_ref, s_ref = oracle.quantize(y, d)
+    q, s = q.cpu().numpy(), s.cpu().numpy()
+    assert np.isinf(s_ref).any() and np.isnan(y).any()
+    assert np.array_equal(np.isinf(s), np.isinf(s_ref)) and not np.isnan(s).any()
+    fin = np.isfinite(s_ref)
+    assert np.abs(s[fin] / s_ref[fin] - 1).max() <= 2 ** -7
+    num = np.isfinite(y)
+    assert np.abs(q[num].astype(np.int32) - q_ref[num].astype(np.int32)).max() <= 1
+    assert (q[num] != q_ref[num]).mean() < 1e-3
+
+
 def test_adaln_quant_matches_unfused(dev):
     """hy_nomas tests/test_fused.py:52-60."""
     from hy_nomas import fused, kernels
