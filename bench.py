@@ -576,8 +576,8 @@ def cpu_host():
     return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": affinity}
 
 
-# Threads for the CPU legs: the GPU box grants one GPU's job a 16-CPU share (its worker pools and
-# OMP_NUM_THREADS are sized to it), whatever the host's CPU count.
+# Threads for the CPU legs: a one-GPU job on the MI355X hosts this runs on has a 16-CPU share (its worker
+# pools and OMP_NUM_THREADS are sized to it), whatever the host's CPU count.
 CPU_SHARE = 16
 
 
