@@ -148,6 +148,31 @@ def test_reciprocal_refinement_exhaustive():
     assert oracle.lib().hno_check_reciprocal_refinement() == 0
 
 
+def test_half_even_code_by_magic_add():
+    """The half-even int8 code as the low byte of fp32(y + 1.5 * 2^23) (the device's one-op form) equals the low
+    byte of rint(y), ties to even, for every integer and half-integer in [-128, 128] with its 8 nearest fp32
+    neighbours on each side, every fp32 in [125, 128) and its negative (the largest codes), and 4 million
+    random quotients in [-127.5, 127.5]."""
+    rng = np.random.default_rng(7)
+    ties = np.arange(-256, 257, dtype=np.float32) / np.float32(2)
+    near, up, down = [ties], ties.copy(), ties.copy()
+    for _ in range(8):
+        up = np.nextafter(up, np.float32(np.inf))
+        down = np.nextafter(down, np.float32(-np.inf))
+        near += [up, down]
+    lo = np.frombuffer(np.float32(125.0).tobytes(), np.uint32)[0]
+    hi = np.frombuffer(np.float32(128.0).tobytes(), np.uint32)[0]
+    top = np.arange(lo, hi, dtype=np.uint32).view(np.float32)
+    y = np.concatenate(near + [top, -top, rng.uniform(-127.5, 127.5, 4_000_000).astype(np.float32)])
+    want = (np.rint(y).astype(np.int32) & 0xFF).astype(np.uint8)
+    got = ((y + np.float32(1.5 * 2 ** 23)).view(np.uint32) & 0xFF).astype(np.uint8)
+    assert np.array_equal(got, want)
+    # a planted error must be caught: with 2^23 the negative quotients fall into the binade below, whose
+    # spacing is 1/2, so their low bytes are no longer the codes
+    bad = ((y + np.float32(2 ** 23)).view(np.uint32) & 0xFF).astype(np.uint8)
+    assert not np.array_equal(bad, want)
+
+
 def test_fast_scale_division_exhaustive():
     """The device's group scales peak / 127 and max(peak, 1e-12) / 448 from the reciprocal + FMA quotient
     equal IEEE division for every bf16 peak >= 2^-80."""
